@@ -1,0 +1,181 @@
+"""Throughput benchmark of the MI355X SD1.5 UNet engine (one GPU).
+
+Workload (the headline configuration): batch-CFG UNet forward, B=2 (cond +
+uncond), 2x4x64x64 latent, 2x77x768 context, fp16 storage / fp32 accumulation,
+seeded random-init weights (conv/linear N(0,0.02) fp16, norm gamma 1 / beta 0,
+biases 0).  One step = one full UNet forward; inputs are resident in HBM before
+the timed region.  Also reported: ms per 4-step LCM + CFG denoise (guidance 8),
+a per-kernel profile (HIP events on the engine stream) with the roofline of the
+dominant kernel, and the CPU oracle's fp32 forward timed on this host.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "sd-vulkan-pixel10-tensor-g5_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_MFMA_TFLOPS = 2500.0   # MI355X dense fp16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+METRIC = "UNet forwards/sec (B=2, 64x64, fp16) on 1 MI355X; ms per 4-step LCM denoise"
+
+
+def cpu_baseline(B=2, H=64, W=64, timed=2):
+    """The oracle's fp32 torch forward on the host cores (B=2 64x64 sample)."""
+    import numpy as np
+    import torch
+    from oracle import lcm, unet_ref, weights
+    threads = min(os.cpu_count() or 1, 64)
+    torch.set_num_threads(threads)
+    p = unet_ref.to_torch(weights.generate(1234))
+    lat = weights.gauss("input.latent", (B, 4, H, W), 1, fp16=False)
+    ctx = weights.gauss("input.context", (B, 77, 768), 1, fp16=False)
+    temb = lcm.time_proj(999)
+    ts = []
+    with torch.inference_mode():
+        unet_ref.unet_forward(p, lat, temb, ctx)  # warm-up
+        for _ in range(timed):
+            t0 = time.perf_counter()
+            unet_ref.unet_forward(p, lat, temb, ctx)
+            ts.append(time.perf_counter() - t0)
+    med = float(np.median(ts))
+    return {"value": 1.0 / med, "unit": f"UNet forwards/sec (B={B}, {H}x{W}, fp32, CPU)",
+            "cores": threads, "kind": "port",
+            "sample": f"1 warm-up + median of {timed} B={B} {H}x{W} fp32 forwards of the oracle "
+                      f"({med:.2f} s each)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--lcm-reps", type=int, default=10)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this engine runs on one GPU; multi-GPU runs are not part of this build "
+              "(each GPU would run its own B=2 CFG pairs independently).", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    import sdu
+    from oracle import lcm, weights  # input generation only (same seeded stream as the tests)
+
+    B, H, W, L = 2, 64, 64, 77
+    eng = sdu.Engine(seed=1234)
+    lat = weights.gauss("input.latent", (B, 4, H, W), 1, fp16=False)
+    ctx = weights.gauss("input.context", (B, L, 768), 1, fp16=False)
+    temb = lcm.time_proj(999)
+    d_lat, d_ctx, d_temb = eng.upload(lat), eng.upload(ctx), eng.upload(temb)
+    d_out = eng.tensor((B, 4, H, W), sdu.SDU_F32)
+
+    def fwd():
+        eng.forward_device(d_lat.ptr, d_temb.ptr, d_ctx.ptr, B, H, W, L, d_out.ptr)
+
+    for _ in range(args.warmup):
+        fwd()
+    eng.sync()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        fwd()
+    eng.sync()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    ms_step = dt / args.steps * 1e3
+    fps = args.steps / dt
+    out = d_out.numpy()
+    assert np.isfinite(out).all(), "non-finite UNet output"
+
+    # 4-step LCM + CFG denoise (guidance 8), device-resident
+    steps = 4
+    lat1 = weights.gauss("input.latent", (4, H, W), 2, fp16=False)
+    cond = weights.gauss("input.cond", (L, 768), 2, fp16=False)
+    unc = weights.gauss("input.uncond", (L, 768), 2, fp16=False)
+    noise = weights.gauss("input.noise", (steps - 1, 4, H, W), 2, fp16=False)
+    dl, dc, du, dn = eng.upload(lat1), eng.upload(cond), eng.upload(unc), eng.upload(noise)
+    dlo = eng.tensor((4, H, W), sdu.SDU_F32)
+
+    def den():
+        eng.denoise_lcm_device(dl.ptr, dc.ptr, du.ptr, H, W, L, steps, 8.0, dn.ptr, dlo.ptr)
+
+    for _ in range(2):
+        den()
+    eng.sync()
+    t0 = time.perf_counter()
+    for _ in range(args.lcm_reps):
+        den()
+    eng.sync()
+    lcm_ms = (time.perf_counter() - t0) / args.lcm_reps * 1e3
+
+    # per-kernel profile (HIP events on the engine stream, eager launches)
+    prof, prof_total = eng.profile(B, H, W, L)
+    kernels = {k[2:]: v for k, v in prof.items() if k.startswith("k:")}
+    cats = {k: v for k, v in prof.items() if not k.startswith("k:")}
+    dom_name, dom = max(kernels.items(), key=lambda kv: kv[1]["ms"])
+    if dom["flops"] > 0:
+        ach = dom["flops"] / (dom["ms"] * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(ach / PEAK_MFMA_TFLOPS, 4), "traffic": None,
+                "kernel": dom_name, "calls": dom["calls"],
+                "flops_per_launch": dom["flops"] / dom["calls"],
+                "avg_launch_us": dom["ms"] * 1e3 / dom["calls"]}
+    else:
+        ach = dom["bytes"] / (dom["ms"] * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None,
+                "kernel": dom_name, "calls": dom["calls"],
+                "bytes_per_launch": dom["bytes"] / dom["calls"],
+                "avg_launch_us": dom["ms"] * 1e3 / dom["calls"]}
+    per_kernel = {}
+    for k, v in sorted(kernels.items(), key=lambda kv: -kv[1]["ms"]):
+        e = {"calls": v["calls"], "ms": round(v["ms"], 4)}
+        if v["flops"] > 0:
+            e["tflops"] = round(v["flops"] / (v["ms"] * 1e-3) / 1e12, 1)
+            e["frac_mfma"] = round(e["tflops"] / PEAK_MFMA_TFLOPS, 4)
+        elif v["bytes"] > 0:
+            e["gbs"] = round(v["bytes"] / (v["ms"] * 1e-3) / 1e9, 1)
+            e["frac_hbm"] = round(e["gbs"] / PEAK_HBM_GBS, 4)
+        per_kernel[k] = e
+    per_cat = {k: {"calls": v["calls"], "ms": round(v["ms"], 4)} for k, v in
+               sorted(cats.items(), key=lambda kv: -kv[1]["ms"])}
+
+    cpu = None if args.no_cpu else cpu_baseline()
+    eng.release()
+
+    line = {
+        "metric": METRIC,
+        "value": round(fps, 3),
+        "unit": "UNet forwards/sec",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (seeded N(0,1) latent/context, seeded random-init weights)",
+        "config": {"workload": "SD1.5 UNet forward, batch-CFG B=2, 2x4x64x64 latent, 2x77x768 context",
+                   "global_batch": B, "latent": [H, W], "context_tokens": L, "parallelism": "single GPU"},
+        "lcm_4step_ms": round(lcm_ms, 3),
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "profile_total_ms": round(prof_total, 4),
+        "kernels": per_kernel,
+        "categories": per_cat,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

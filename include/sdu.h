@@ -1,0 +1,191 @@
+/*
+ * sdu.h -- C ABI of the MI355X (gfx950) SD1.5 UNet engine.
+ *
+ * Drop-in for the reference's Vulkan engine boundary: the JNI entry points of
+ * app/src/main/cpp/vk_engine.cpp (declared in sd/VulkanBench.kt:22-27) and the
+ * op-level interface of its `namespace unet` (vk_engine.cpp:487-790), without the
+ * JVM.  Plain pointers and sizes only; no C++ or torch types cross this line.
+ *
+ * Conventions
+ *  - Every entry point returns an int status (SDU_OK == 0, negative on error) and
+ *    never throws; sdu_last_error() returns the message of the last failure.
+ *  - One sdu_ctx owns one HIP stream, the resident fp16 weights and an activation
+ *    arena.  A context is not thread-safe: call it from one thread at a time
+ *    (the reference runs every call on one GpuThread, GenerateViewModel.kt:31).
+ *  - Host-buffer entry points are synchronous.  *_device entry points enqueue on
+ *    the context stream and return; sdu_synchronize() waits.
+ *  - Host tensors at the UNet boundary are float32 NCHW, as the reference's JNI
+ *    byte arrays are (vk_engine.cpp:874-887).  Inside, activations are fp16 NHWC.
+ */
+#ifndef SDU_H
+#define SDU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct sdu_ctx sdu_ctx;
+typedef struct sdu_tensor sdu_tensor;
+
+enum sdu_status {
+    SDU_OK = 0,
+    SDU_ERR_DEVICE = -1,     /* device init failed (unetInit's -1, vk_engine.cpp:801) */
+    SDU_ERR_NOT_INIT = -2,   /* no context (unetSelfTest's -2, vk_engine.cpp:813)     */
+    SDU_ERR_ARG = -3,        /* bad pointer, size or shape                            */
+    SDU_ERR_WEIGHT = -4,     /* missing / short weight file or unknown weight name    */
+    SDU_ERR_IO = -5,         /* file could not be read                                */
+    SDU_ERR_OOM = -6,        /* device allocation failed                              */
+    SDU_ERR_HIP = -7         /* a HIP runtime call failed                             */
+};
+
+enum sdu_dtype { SDU_F16 = 1, SDU_F32 = 2 };
+
+/* sdu_init flags */
+#define SDU_INIT_RANDOM_AFFINE 0x1 /* seeded weights: biases/betas N(0,.02), gammas N(1,.02) */
+#define SDU_INIT_NO_WEIGHTS    0x2 /* op-level use only: no UNet weights are created      */
+
+/* ---------------------------------------------------------------- lifecycle */
+
+/* unetInit (vk_engine.cpp:796-808).  weights_dir == NULL: seeded random-init
+ * weights (conv/linear fp16(N(0,0.02)), norm gamma 1 / beta 0, biases 0).
+ * Otherwise every tensor is read from <dir>/<diffusers key>.bin, raw fp16 LE, the
+ * reference's unet_w/ layout (Linear stored [in,out]); a missing or short file is
+ * an error (SDU_ERR_WEIGHT), not a silent zero tensor as in vk_engine.cpp:500-505. */
+int sdu_init(sdu_ctx** out, const char* weights_dir, uint64_t seed, int flags);
+/* unetRelease (vk_engine.cpp:915-926).  NULL is accepted. */
+int sdu_release(sdu_ctx* ctx);
+const char* sdu_last_error(const sdu_ctx* ctx);
+int sdu_synchronize(sdu_ctx* ctx);
+
+/* Replace / read one UNet weight, given in its canonical diffusers layout
+ * (conv [Co,Ci,kh,kw], Linear [out,in]) as float32 host data (rounded to fp16). */
+int sdu_set_weight(sdu_ctx* ctx, const char* name, const float* data, int64_t numel);
+int sdu_get_weight(sdu_ctx* ctx, const char* name, float* out, int64_t numel);
+/* Number of UNet parameters (859,520,964 for SD1.5) and of named tensors. */
+int sdu_param_count(sdu_ctx* ctx, int64_t* n_params, int64_t* n_tensors);
+
+/* ------------------------------------------------------------ UNet forward */
+
+/* unetForward (vk_engine.cpp:875-887), generalised to explicit shapes.
+ * lat [B,4,H,W], temb [320] (sinusoid-projected timestep, shared by the batch as
+ * tembp is, vk_engine.cpp:715-717), ctx [B,L,768]  ->  out [B,4,H,W].
+ * H, W multiples of 8; 1 <= B <= 64; 1 <= L <= 256. */
+int sdu_forward(sdu_ctx* ctx, const float* lat, const float* temb, const float* ctx_emb,
+                int B, int H, int W, int L, float* out);
+
+/* unetForward2 (vk_engine.cpp:891-913): one latent shared by the cond and uncond
+ * slots (B=2), ctx = [cond; uncond]; out = [cond eps | uncond eps], each [4,H,W]. */
+int sdu_forward_cfg(sdu_ctx* ctx, const float* lat, const float* temb, const float* cond,
+                    const float* uncond, int H, int W, int L, float* out);
+
+/* Full LCM + batch-CFG denoise (VulkanUnetPipeline.kt:63-97 with
+ * LcmScheduler.kt:56-82) on the device: lat [4,H,W] -> out [4,H,W].
+ * noise [steps-1,4,H,W] is the injected per-step noise (the reference draws it
+ * from its RNG at :87).  guidance is the CFG scale (u + s (c - u)). */
+int sdu_denoise_lcm(sdu_ctx* ctx, const float* lat, const float* cond, const float* uncond,
+                    int H, int W, int L, int steps, float guidance, const float* noise,
+                    float* out);
+
+/* Device-resident variants for throughput runs: every pointer is device memory
+ * (same layouts and dtypes as above).  Enqueued on the context stream; the first
+ * call for a shape records a HIP graph, later calls replay it. */
+int sdu_forward_device(sdu_ctx* ctx, const float* d_lat, const float* d_temb,
+                       const float* d_ctx, int B, int H, int W, int L, float* d_out);
+int sdu_denoise_lcm_device(sdu_ctx* ctx, const float* d_lat, const float* d_cond,
+                           const float* d_uncond, int H, int W, int L, int steps,
+                           float guidance, const float* d_noise, float* d_out);
+
+/* unetSelfTest (vk_engine.cpp:811-851): reads fixture_dir/IN_lat.bin (fp16 [4,64,64]),
+ * IN_ctx.bin (fp16 [77,768]), IN_temb_proj.bin (fp16 [320]) and OUT_y.bin (fp16),
+ * runs B=1 and B=2 (same input in both slots) and returns the largest
+ * relErr_L1 = sum|ref-got| / sum|ref| over the three outputs; negative on error. */
+double sdu_selftest(sdu_ctx* ctx, const char* fixture_dir);
+
+/* unetProfile (vk_engine.cpp:854-872): one eager forward, each kernel timed with
+ * HIP events on the context stream, accumulated per category. */
+typedef struct sdu_prof_entry {
+    char name[32];
+    int calls;
+    double ms;      /* summed kernel time */
+    double flops;   /* algorithmic FLOPs over those calls */
+    double bytes;   /* algorithmic HBM bytes over those calls */
+} sdu_prof_entry;
+int sdu_profile(sdu_ctx* ctx, int B, int H, int W, int L, sdu_prof_entry* out,
+                int max_entries, int* n_entries, double* total_ms);
+
+/* ------------------------------------------------------------- tensors */
+
+int sdu_tensor_alloc(sdu_ctx* ctx, int dtype, int ndim, const int64_t* shape, sdu_tensor** out);
+int sdu_tensor_free(sdu_ctx* ctx, sdu_tensor* t);
+int sdu_tensor_upload(sdu_ctx* ctx, sdu_tensor* t, const void* host, size_t bytes);
+int sdu_tensor_download(sdu_ctx* ctx, const sdu_tensor* t, void* host, size_t bytes);
+void* sdu_tensor_device_ptr(const sdu_tensor* t);
+size_t sdu_tensor_bytes(const sdu_tensor* t);
+
+/* ---------------------------------------------------------------- ops
+ * The reference's `namespace unet` ops (vk_engine.cpp:547-613) with explicit
+ * batch and shapes instead of the global gB.  fp16 tensors unless stated,
+ * activations NHWC ([B, H*W, C] row-major = tokens x channels). */
+
+/* groupnorm / groupnorm_silu (vk_engine.cpp:548-549): per-image statistics over
+ * `groups` channel groups.  x2 (may be NULL) is a second source concatenated
+ * along channels (C = C1 + C2) -- the up-path skip concat (vk_engine.cpp:678-688)
+ * without materialising it.  gamma/beta fp16 [C]. */
+int sdu_groupnorm(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* x2, const sdu_tensor* gamma,
+                  const sdu_tensor* beta, sdu_tensor* y, int B, int HW, int C1, int C2,
+                  int groups, float eps, int silu);
+
+/* LN (vk_engine.cpp:652): y[t,:] = LN(x[t,:]) over C. */
+int sdu_layernorm(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* gamma, const sdu_tensor* beta,
+                  sdu_tensor* y, int T, int C, float eps);
+
+/* Epilogue flags for sdu_matmul / sdu_conv2d */
+#define SDU_EPI_GEGLU   0x1 /* w rows interleaved per 32 (a,b); y[:, N/2] = a * gelu_erf(b)   */
+#define SDU_EPI_OUT_F32 0x2 /* y is float32                                                    */
+
+/* matmul (vk_engine.cpp:612-613) with fused epilogue:
+ * y[M,N] = a[M,K] . w[N,K]^T (+ bias[N]) (+ residual[M,N]).
+ * a2 (may be NULL) supplies columns [K1, K) of a (a = [a | a2], K1 = K - K2):
+ * the 1x1 shortcut over a concatenated input. */
+int sdu_matmul(sdu_ctx* ctx, const sdu_tensor* a, const sdu_tensor* a2, const sdu_tensor* w,
+               const sdu_tensor* bias, const sdu_tensor* residual, sdu_tensor* y,
+               int M, int N, int K, int K2, int flags);
+
+/* conv (vk_engine.cpp:578-608) as implicit GEMM: x NHWC [B,H,W,Ci], w [Co,k,k,Ci]
+ * (k = 1 or 3, pad k/2), stride 1 or 2, optional nearest-2x upsample of the input
+ * (upsample(), vk_engine.cpp:693-697).  y NHWC [B,Ho,Wo,Co] (+bias[Co])
+ * (+ temb[Co] float32 broadcast, the resnet's time projection, :630)
+ * (+ residual NHWC [B,Ho,Wo,Co]). */
+int sdu_conv2d(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* w, const sdu_tensor* bias,
+               const sdu_tensor* temb, const sdu_tensor* residual, sdu_tensor* y, int B, int H,
+               int W, int Ci, int Co, int ksize, int stride, int upsample, int flags);
+
+/* ATTN / ATTN_BIG (vk_engine.cpp:655, :663): per image b and head h,
+ * o = softmax(q k^T * scale) v.  q rows b*Sq+i, k/v rows b*Sk+j, head h at column
+ * h*d; ldq/ldk/ldv/ldo are row strides in elements.  d in {8,...,160}, d % 8 == 0. */
+int sdu_attention(sdu_ctx* ctx, const sdu_tensor* q, const sdu_tensor* k, const sdu_tensor* v,
+                  sdu_tensor* o, int B, int heads, int Sq, int Sk, int d, int ldq, int ldk,
+                  int ldv, int ldo, float scale);
+
+/* GEGLU (geglu_f32.comp): y[t,c] = g[t,c] * gelu_erf(g[t,C2+c]). */
+int sdu_geglu(sdu_ctx* ctx, const sdu_tensor* g, sdu_tensor* y, int T, int C2);
+/* SILU (silu_f32.comp), ADD (add_f32.comp) and AB/AB2 (addbias_f32.comp,
+ * addbias2_f32.comp; y[i] += b[i % C]) on n elements. */
+int sdu_silu(sdu_ctx* ctx, const sdu_tensor* x, sdu_tensor* y, int64_t n);
+int sdu_add(sdu_ctx* ctx, const sdu_tensor* a, const sdu_tensor* b, sdu_tensor* y, int64_t n);
+int sdu_add_bias(sdu_ctx* ctx, sdu_tensor* y, const sdu_tensor* bias, int64_t n, int C);
+
+/* LcmScheduler.step (LcmScheduler.kt:56-82) fused with the CFG combine
+ * (VulkanUnetPipeline.kt:86).  float32 tensors: x [n] (updated in place),
+ * eps2 [2, n] (cond then uncond), noise [n] (NULL on the last step).
+ * The coefficients come from the schedule of `steps` steps at step `idx`. */
+int sdu_lcm_step(sdu_ctx* ctx, sdu_tensor* x, const sdu_tensor* eps2, const sdu_tensor* noise,
+                 int64_t n, int steps, int idx, float guidance);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SDU_H */

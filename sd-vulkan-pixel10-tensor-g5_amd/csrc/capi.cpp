@@ -1,0 +1,522 @@
+// extern "C" entry points of include/sdu.h.  Every function validates its
+// arguments, returns a status code and never lets an exception cross the ABI.
+#include "engine.h"
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <new>
+
+using namespace sdu;
+
+namespace {
+
+thread_local std::string g_noctx_err;
+
+int fail(sdu_ctx* c, int code, const std::string& msg) {
+    if (c) c->c.err = msg;
+    else g_noctx_err = msg;
+    return code;
+}
+
+int hipfail(sdu_ctx* c, hipError_t e, const char* what) {
+    return fail(c, SDU_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define SDU_GUARD(ctx)                                                   \
+    if (!(ctx)) return fail(nullptr, SDU_ERR_NOT_INIT, "null context");
+
+template <class F>
+int guarded(sdu_ctx* ctx, F&& f) {
+    try {
+        return f();
+    } catch (const std::bad_alloc&) {
+        return fail(ctx, SDU_ERR_OOM, "host allocation failed");
+    } catch (...) {
+        return fail(ctx, SDU_ERR_ARG, "unexpected exception");
+    }
+}
+
+const void* dptr(const sdu_tensor* t) { return t ? t->t.ptr : nullptr; }
+void* dptr(sdu_tensor* t) { return t ? t->t.ptr : nullptr; }
+
+bool fits(const sdu_tensor* t, size_t bytes) { return t && t->t.bytes >= bytes; }
+
+int finish(sdu_ctx* ctx, hipError_t e, const char* what) {
+    if (e != hipSuccess) return hipfail(ctx, e, what);
+    return SDU_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sdu_init(sdu_ctx** out, const char* weights_dir, uint64_t seed, int flags) {
+    if (!out) return fail(nullptr, SDU_ERR_ARG, "out is null");
+    *out = nullptr;
+    return guarded(nullptr, [&]() -> int {
+        int ndev = 0;
+        if (hipGetDeviceCount(&ndev) != hipSuccess || ndev < 1)
+            return fail(nullptr, SDU_ERR_DEVICE, "no HIP device");
+        std::unique_ptr<sdu_ctx> h(new sdu_ctx());
+        Ctx& c = h->c;
+        c.seed = seed;
+        c.flags = flags;
+        hipError_t e = hipGetDevice(&c.device);
+        if (e == hipSuccess) e = hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking);
+        if (e != hipSuccess) return fail(nullptr, SDU_ERR_DEVICE, std::string("stream: ") + hipGetErrorString(e));
+        if (!(flags & SDU_INIT_NO_WEIGHTS)) {
+            int st = build_inventory(c);
+            if (!st) st = weights_dir ? init_weights_dir(c, weights_dir) : init_weights_seeded(c);
+            if (st) {
+                g_noctx_err = c.err;
+                if (c.wpool) hipFree(c.wpool);
+                hipStreamDestroy(c.stream);
+                return st;
+            }
+        }
+        *out = h.release();
+        return SDU_OK;
+    });
+}
+
+int sdu_release(sdu_ctx* ctx) {
+    if (!ctx) return SDU_OK;
+    Ctx& c = ctx->c;
+    hipStreamSynchronize(c.stream);
+    free_fwd_states(c);
+    if (c.wpool) hipFree(c.wpool);
+    if (c.op_ws) hipFree(c.op_ws);
+    hipStreamDestroy(c.stream);
+    delete ctx;
+    return SDU_OK;
+}
+
+const char* sdu_last_error(const sdu_ctx* ctx) {
+    return ctx ? ctx->c.err.c_str() : g_noctx_err.c_str();
+}
+
+int sdu_synchronize(sdu_ctx* ctx) {
+    SDU_GUARD(ctx);
+    return finish(ctx, hipStreamSynchronize(ctx->c.stream), "synchronize");
+}
+
+int sdu_set_weight(sdu_ctx* ctx, const char* name, const float* data, int64_t numel) {
+    SDU_GUARD(ctx);
+    if (!name || !data) return fail(ctx, SDU_ERR_ARG, "null argument");
+    return guarded(ctx, [&]() -> int {
+        const WeightRec* r = ctx->c.w(name);
+        if (!r) return fail(ctx, SDU_ERR_WEIGHT, std::string("unknown weight: ") + name);
+        if (numel != r->numel()) return fail(ctx, SDU_ERR_ARG, std::string("numel mismatch for ") + name);
+        hipStreamSynchronize(ctx->c.stream);
+        return set_weight_canonical(ctx->c, *r, data);
+    });
+}
+
+int sdu_get_weight(sdu_ctx* ctx, const char* name, float* out, int64_t numel) {
+    SDU_GUARD(ctx);
+    if (!name || !out) return fail(ctx, SDU_ERR_ARG, "null argument");
+    return guarded(ctx, [&]() -> int {
+        const WeightRec* r = ctx->c.w(name);
+        if (!r) return fail(ctx, SDU_ERR_WEIGHT, std::string("unknown weight: ") + name);
+        if (numel != r->numel()) return fail(ctx, SDU_ERR_ARG, std::string("numel mismatch for ") + name);
+        hipStreamSynchronize(ctx->c.stream);
+        return get_weight_canonical(ctx->c, *r, out);
+    });
+}
+
+int sdu_param_count(sdu_ctx* ctx, int64_t* n_params, int64_t* n_tensors) {
+    SDU_GUARD(ctx);
+    int64_t n = 0;
+    for (const WeightRec& r : ctx->c.weights) n += r.numel();
+    if (n_params) *n_params = n;
+    if (n_tensors) *n_tensors = (int64_t)ctx->c.weights.size();
+    return SDU_OK;
+}
+
+int sdu_forward(sdu_ctx* ctx, const float* lat, const float* temb, const float* ctx_emb, int B, int H,
+                int W, int L, float* out) {
+    SDU_GUARD(ctx);
+    if (!lat || !temb || !ctx_emb || !out) return fail(ctx, SDU_ERR_ARG, "null argument");
+    return guarded(ctx, [&] { return unet_forward_host(ctx->c, lat, temb, ctx_emb, B, H, W, L, out); });
+}
+
+int sdu_forward_cfg(sdu_ctx* ctx, const float* lat, const float* temb, const float* cond,
+                    const float* uncond, int H, int W, int L, float* out) {
+    SDU_GUARD(ctx);
+    if (!lat || !temb || !cond || !uncond || !out) return fail(ctx, SDU_ERR_ARG, "null argument");
+    return guarded(ctx, [&]() -> int {
+        // unetForward2 (vk_engine.cpp:891-913): duplicate the latent, stack [cond; uncond]
+        const size_t n = (size_t)4 * H * W, cl = (size_t)L * 768;
+        if (H <= 0 || W <= 0 || L <= 0) return fail(ctx, SDU_ERR_ARG, "bad shape");
+        std::vector<float> lat2(2 * n), ctx2(2 * cl);
+        memcpy(lat2.data(), lat, n * 4);
+        memcpy(lat2.data() + n, lat, n * 4);
+        memcpy(ctx2.data(), cond, cl * 4);
+        memcpy(ctx2.data() + cl, uncond, cl * 4);
+        return unet_forward_host(ctx->c, lat2.data(), temb, ctx2.data(), 2, H, W, L, out);
+    });
+}
+
+int sdu_forward_device(sdu_ctx* ctx, const float* d_lat, const float* d_temb, const float* d_ctx, int B,
+                       int H, int W, int L, float* d_out) {
+    SDU_GUARD(ctx);
+    if (!d_lat || !d_temb || !d_ctx || !d_out) return fail(ctx, SDU_ERR_ARG, "null argument");
+    return guarded(ctx, [&] { return unet_forward_device(ctx->c, d_lat, d_temb, d_ctx, B, H, W, L, d_out); });
+}
+
+int sdu_denoise_lcm_device(sdu_ctx* ctx, const float* d_lat, const float* d_cond, const float* d_uncond,
+                           int H, int W, int L, int steps, float guidance, const float* d_noise,
+                           float* d_out) {
+    SDU_GUARD(ctx);
+    if (!d_lat || !d_cond || !d_uncond || !d_out) return fail(ctx, SDU_ERR_ARG, "null argument");
+    return guarded(ctx, [&] {
+        return unet_denoise_device(ctx->c, d_lat, d_cond, d_uncond, H, W, L, steps, guidance, d_noise, d_out);
+    });
+}
+
+int sdu_denoise_lcm(sdu_ctx* ctx, const float* lat, const float* cond, const float* uncond, int H, int W,
+                    int L, int steps, float guidance, const float* noise, float* out) {
+    SDU_GUARD(ctx);
+    if (!lat || !cond || !uncond || !out || (steps > 1 && !noise)) return fail(ctx, SDU_ERR_ARG, "null argument");
+    if (H <= 0 || W <= 0 || L <= 0 || steps < 1 || steps > 50) return fail(ctx, SDU_ERR_ARG, "bad shape");
+    return guarded(ctx, [&]() -> int {
+        const size_t n = (size_t)4 * H * W, cl = (size_t)L * 768;
+        const size_t nn = steps > 1 ? (size_t)(steps - 1) * n : 0;
+        float* d = nullptr;
+        const size_t tot = n + 2 * cl + nn + n;
+        hipError_t e = hipMalloc(&d, tot * 4);
+        if (e != hipSuccess) return fail(ctx, SDU_ERR_OOM, "staging allocation failed");
+        float *dl = d, *dc = d + n, *du = dc + cl, *dn = du + cl, *dout = dn + nn;
+        hipStream_t s = ctx->c.stream;
+        int st = SDU_OK;
+        if ((e = hipMemcpyAsync(dl, lat, n * 4, hipMemcpyHostToDevice, s)) ||
+            (e = hipMemcpyAsync(dc, cond, cl * 4, hipMemcpyHostToDevice, s)) ||
+            (e = hipMemcpyAsync(du, uncond, cl * 4, hipMemcpyHostToDevice, s)) ||
+            (nn && (e = hipMemcpyAsync(dn, noise, nn * 4, hipMemcpyHostToDevice, s))))
+            st = hipfail(ctx, e, "upload");
+        if (!st) st = unet_denoise_device(ctx->c, dl, dc, du, H, W, L, steps, guidance, nn ? dn : nullptr, dout);
+        if (!st && ((e = hipMemcpyAsync(out, dout, n * 4, hipMemcpyDeviceToHost, s)) ||
+                    (e = hipStreamSynchronize(s))))
+            st = hipfail(ctx, e, "download");
+        hipStreamSynchronize(s);
+        hipFree(d);
+        return st;
+    });
+}
+
+double sdu_selftest(sdu_ctx* ctx, const char* fixture_dir) {
+    if (!ctx) return (double)SDU_ERR_NOT_INIT;
+    if (!fixture_dir) return (double)fail(ctx, SDU_ERR_ARG, "null fixture dir");
+    try {
+        // unetSelfTest protocol (vk_engine.cpp:811-839): fp16 IN_lat / IN_ctx /
+        // IN_temb_proj, B=1 forward vs OUT_y, then B=2 with the input in both slots.
+        auto load = [&](const char* nm, size_t n, std::vector<float>& v) -> bool {
+            std::ifstream f(std::string(fixture_dir) + "/" + nm + ".bin", std::ios::binary);
+            if (!f) return false;
+            std::vector<f16> h(n);
+            if (!f.read((char*)h.data(), n * 2)) return false;
+            v.resize(n);
+            for (size_t i = 0; i < n; ++i) v[i] = (float)h[i];
+            return true;
+        };
+        const size_t HW = 64 * 64, LAT = 4 * HW, CTX = 77 * 768;
+        std::vector<float> lat, cx, tp, ref;
+        if (!load("IN_lat", LAT, lat) || !load("IN_ctx", CTX, cx) || !load("IN_temb_proj", 320, tp) ||
+            !load("OUT_y", LAT, ref))
+            return (double)fail(ctx, SDU_ERR_IO, "self-test fixture missing");
+        auto rel = [&](const float* got) {
+            double se = 0, sr = 0;
+            for (size_t i = 0; i < LAT; ++i) { se += std::fabs(ref[i] - got[i]); sr += std::fabs(ref[i]); }
+            return se / (sr + 1e-6);
+        };
+        std::vector<float> y1(LAT), y2(2 * LAT);
+        int st = unet_forward_host(ctx->c, lat.data(), tp.data(), cx.data(), 1, 64, 64, 77, y1.data());
+        if (st) return (double)st;
+        std::vector<float> lat2(2 * LAT), cx2(2 * CTX);
+        memcpy(lat2.data(), lat.data(), LAT * 4);
+        memcpy(lat2.data() + LAT, lat.data(), LAT * 4);
+        memcpy(cx2.data(), cx.data(), CTX * 4);
+        memcpy(cx2.data() + CTX, cx.data(), CTX * 4);
+        st = unet_forward_host(ctx->c, lat2.data(), tp.data(), cx2.data(), 2, 64, 64, 77, y2.data());
+        if (st) return (double)st;
+        const double e0 = rel(y1.data()), e1 = rel(y2.data()), e2 = rel(y2.data() + LAT);
+        return std::max(e0, std::max(e1, e2));
+    } catch (...) {
+        return (double)fail(ctx, SDU_ERR_OOM, "self-test failed");
+    }
+}
+
+int sdu_profile(sdu_ctx* ctx, int B, int H, int W, int L, sdu_prof_entry* out, int max_entries,
+                int* n_entries, double* total_ms) {
+    SDU_GUARD(ctx);
+    return guarded(ctx, [&]() -> int {
+        int st = unet_profile(ctx->c, B, H, W, L);
+        if (st) return st;
+        int n = 0;
+        double tot = 0;
+        for (auto& kv : ctx->c.prof) {
+            if (kv.first.rfind("k:", 0) != 0) tot += kv.second.ms;
+            if (out && n < max_entries) {
+                sdu_prof_entry& e = out[n];
+                memset(&e, 0, sizeof e);
+                snprintf(e.name, sizeof e.name, "%s", kv.first.c_str());
+                e.calls = kv.second.calls;
+                e.ms = kv.second.ms;
+                e.flops = kv.second.flops;
+                e.bytes = kv.second.bytes;
+            }
+            ++n;
+        }
+        if (n_entries) *n_entries = n;
+        if (total_ms) *total_ms = tot;
+        return SDU_OK;
+    });
+}
+
+// ---------------------------------------------------------------- tensors
+
+int sdu_tensor_alloc(sdu_ctx* ctx, int dtype, int ndim, const int64_t* shape, sdu_tensor** out) {
+    SDU_GUARD(ctx);
+    if (!out || ndim < 0 || ndim > 8 || (ndim && !shape) || (dtype != SDU_F16 && dtype != SDU_F32))
+        return fail(ctx, SDU_ERR_ARG, "bad tensor description");
+    *out = nullptr;
+    return guarded(ctx, [&]() -> int {
+        int64_t n = 1;
+        for (int i = 0; i < ndim; ++i) {
+            if (shape[i] < 0) return fail(ctx, SDU_ERR_ARG, "negative dimension");
+            n *= shape[i];
+        }
+        std::unique_ptr<sdu_tensor> t(new sdu_tensor());
+        t->t.dtype = dtype;
+        t->t.shape.assign(shape, shape + ndim);
+        t->t.bytes = (size_t)n * (dtype == SDU_F16 ? 2 : 4);
+        if (t->t.bytes) {
+            hipError_t e = hipMalloc(&t->t.ptr, t->t.bytes);
+            if (e != hipSuccess) return fail(ctx, SDU_ERR_OOM, "tensor allocation failed");
+        }
+        *out = t.release();
+        return SDU_OK;
+    });
+}
+
+int sdu_tensor_free(sdu_ctx* ctx, sdu_tensor* t) {
+    SDU_GUARD(ctx);
+    if (!t) return SDU_OK;
+    hipStreamSynchronize(ctx->c.stream);
+    if (t->t.ptr) hipFree(t->t.ptr);
+    delete t;
+    return SDU_OK;
+}
+
+int sdu_tensor_upload(sdu_ctx* ctx, sdu_tensor* t, const void* host, size_t bytes) {
+    SDU_GUARD(ctx);
+    if (!t || (!host && bytes) || bytes > t->t.bytes) return fail(ctx, SDU_ERR_ARG, "bad upload");
+    hipError_t e = hipMemcpyAsync(t->t.ptr, host, bytes, hipMemcpyHostToDevice, ctx->c.stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->c.stream);
+    return finish(ctx, e, "upload");
+}
+
+int sdu_tensor_download(sdu_ctx* ctx, const sdu_tensor* t, void* host, size_t bytes) {
+    SDU_GUARD(ctx);
+    if (!t || (!host && bytes) || bytes > t->t.bytes) return fail(ctx, SDU_ERR_ARG, "bad download");
+    hipError_t e = hipMemcpyAsync(host, t->t.ptr, bytes, hipMemcpyDeviceToHost, ctx->c.stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->c.stream);
+    return finish(ctx, e, "download");
+}
+
+void* sdu_tensor_device_ptr(const sdu_tensor* t) { return t ? t->t.ptr : nullptr; }
+size_t sdu_tensor_bytes(const sdu_tensor* t) { return t ? t->t.bytes : 0; }
+
+// ---------------------------------------------------------------- ops
+
+int sdu_groupnorm(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* x2, const sdu_tensor* gamma,
+                  const sdu_tensor* beta, sdu_tensor* y, int B, int HW, int C1, int C2, int groups,
+                  float eps, int silu) {
+    SDU_GUARD(ctx);
+    const int C = C1 + C2;
+    if (B < 1 || B > 64 || HW < 1 || C1 < 8 || C2 < 0 || groups < 1 || groups > 32 || C % groups ||
+        C1 % 8 || C2 % 8 || (C2 && !x2))
+        return fail(ctx, SDU_ERR_ARG, "bad groupnorm shape");
+    const size_t px = (size_t)B * HW;
+    if (!fits(x, px * C1 * 2) || (C2 && !fits(x2, px * C2 * 2)) || !fits(gamma, (size_t)C * 2) ||
+        !fits(beta, (size_t)C * 2) || !fits(y, px * C * 2))
+        return fail(ctx, SDU_ERR_ARG, "groupnorm tensor too small");
+    if (C > 2560) return fail(ctx, SDU_ERR_ARG, "groupnorm supports C <= 2560");
+    const size_t acc = groupnorm_acc_bytes(B, groups);
+    int st = ensure_op_ws(ctx->c, acc);
+    if (st) return st;
+    hipError_t e = zero_launch(ctx->c.op_ws, acc, ctx->c.stream);
+    if (e == hipSuccess)
+        e = groupnorm_launch((const f16*)dptr(x), (const f16*)dptr(x2), C1, C2, (const f16*)dptr(gamma),
+                             (const f16*)dptr(beta), (f16*)dptr(y), B, HW, groups, eps, silu,
+                             (double*)ctx->c.op_ws, ctx->c.stream);
+    return finish(ctx, e, "groupnorm");
+}
+
+int sdu_layernorm(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* gamma, const sdu_tensor* beta,
+                  sdu_tensor* y, int T, int C, float eps) {
+    SDU_GUARD(ctx);
+    if (T < 1 || C < 8 || C % 8 || C > 2048) return fail(ctx, SDU_ERR_ARG, "bad layernorm shape");
+    if (!fits(x, (size_t)T * C * 2) || !fits(y, (size_t)T * C * 2) || !fits(gamma, (size_t)C * 2) ||
+        !fits(beta, (size_t)C * 2))
+        return fail(ctx, SDU_ERR_ARG, "layernorm tensor too small");
+    return finish(ctx, layernorm_launch((const f16*)dptr(x), (const f16*)dptr(gamma), (const f16*)dptr(beta),
+                                        (f16*)dptr(y), T, C, eps, ctx->c.stream),
+                  "layernorm");
+}
+
+int sdu_matmul(sdu_ctx* ctx, const sdu_tensor* a, const sdu_tensor* a2, const sdu_tensor* w,
+               const sdu_tensor* bias, const sdu_tensor* residual, sdu_tensor* y, int M, int N, int K,
+               int K2, int flags) {
+    SDU_GUARD(ctx);
+    const int geglu = (flags & SDU_EPI_GEGLU) != 0;
+    const int f32 = (flags & SDU_EPI_OUT_F32) != 0;
+    const int K1 = K - K2;
+    if (M < 1 || N < 1 || K < 8 || K % 8 || K2 < 0 || K2 > K || K1 % 8 || (K2 && !a2) ||
+        (geglu && N % 64))
+        return fail(ctx, SDU_ERR_ARG, "bad matmul shape");
+    const int Nout = geglu ? N / 2 : N;
+    if (!fits(a, (size_t)M * K1 * 2) || (K2 && !fits(a2, (size_t)M * K2 * 2)) || !fits(w, (size_t)N * K * 2) ||
+        (bias && !fits(bias, (size_t)N * 2)) || (residual && !fits(residual, (size_t)M * Nout * 2)) ||
+        !fits(y, (size_t)M * Nout * (f32 ? 4 : 2)))
+        return fail(ctx, SDU_ERR_ARG, "matmul tensor too small");
+    GemmArgs g{};
+    g.M = M; g.N = N; g.K = K;
+    g.amode = A_DENSE;
+    g.A = (const f16*)dptr(a); g.lda = K1;
+    g.A2 = K2 ? (const f16*)dptr(a2) : nullptr; g.lda2 = K2; g.K1 = K1;
+    g.Wt = (const f16*)dptr(w);
+    g.bias = (const f16*)dptr(bias);
+    g.res = (const f16*)dptr(residual); g.ldr = Nout;
+    g.C = dptr(y); g.ldc = Nout;
+    g.out_mode = f32 ? OUT_F32 : OUT_F16;
+    g.geglu = geglu;
+    int st = ensure_op_ws(ctx->c, gemm_workspace_bytes(g) + 256);
+    if (st) return st;
+    return finish(ctx, gemm_launch(g, ctx->c.op_ws, ctx->c.stream), "matmul");
+}
+
+int sdu_conv2d(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* w, const sdu_tensor* bias,
+               const sdu_tensor* temb, const sdu_tensor* residual, sdu_tensor* y, int B, int H, int W,
+               int Ci, int Co, int ksize, int stride, int upsample, int flags) {
+    SDU_GUARD(ctx);
+    const int f32 = (flags & SDU_EPI_OUT_F32) != 0;
+    if (B < 1 || H < 1 || W < 1 || Ci < 8 || Ci % 8 || Co < 1 || (ksize != 1 && ksize != 3) ||
+        (stride != 1 && stride != 2) || (upsample && stride != 1) || (ksize == 1 && (stride != 1 || upsample)) ||
+        (flags & SDU_EPI_GEGLU))
+        return fail(ctx, SDU_ERR_ARG, "bad conv2d shape");
+    const int Ho = upsample ? 2 * H : (stride == 2 ? (H - 1) / 2 + 1 : H);
+    const int Wo = upsample ? 2 * W : (stride == 2 ? (W - 1) / 2 + 1 : W);
+    const size_t Mo = (size_t)B * Ho * Wo;
+    if (!fits(x, (size_t)B * H * W * Ci * 2) || !fits(w, (size_t)Co * ksize * ksize * Ci * 2) ||
+        (bias && !fits(bias, (size_t)Co * 2)) || (temb && !fits(temb, (size_t)Co * 4)) ||
+        (residual && !fits(residual, Mo * Co * 2)) || !fits(y, Mo * Co * (f32 ? 4 : 2)) ||
+        (temb && temb->t.dtype != SDU_F32))
+        return fail(ctx, SDU_ERR_ARG, "conv2d tensor too small");
+    GemmArgs g{};
+    g.M = (int)Mo; g.N = Co;
+    if (ksize == 1) {
+        g.amode = A_DENSE;
+        g.K = Ci; g.K1 = Ci;
+        g.A = (const f16*)dptr(x); g.lda = Ci;
+    } else {
+        g.amode = A_CONV3;
+        g.K = 9 * Ci;
+        g.A = (const f16*)dptr(x);
+        g.Bn = B; g.Hin = H; g.Win = W; g.Cin = Ci; g.Ho = Ho; g.Wo = Wo;
+        g.stride = stride; g.upsample = upsample;
+    }
+    g.Wt = (const f16*)dptr(w);
+    g.bias = (const f16*)dptr(bias);
+    g.bias2 = (const float*)dptr(temb);
+    g.res = (const f16*)dptr(residual); g.ldr = Co;
+    g.C = dptr(y); g.ldc = Co;
+    g.out_mode = f32 ? OUT_F32 : OUT_F16;
+    int st = ensure_op_ws(ctx->c, gemm_workspace_bytes(g) + 256);
+    if (st) return st;
+    return finish(ctx, gemm_launch(g, ctx->c.op_ws, ctx->c.stream), "conv2d");
+}
+
+int sdu_attention(sdu_ctx* ctx, const sdu_tensor* q, const sdu_tensor* k, const sdu_tensor* v,
+                  sdu_tensor* o, int B, int heads, int Sq, int Sk, int d, int ldq, int ldk, int ldv,
+                  int ldo, float scale) {
+    SDU_GUARD(ctx);
+    if (B < 1 || heads < 1 || Sq < 1 || Sk < 1 || d < 8 || d > 160 || d % 8 || ldq < heads * d ||
+        ldk < heads * d || ldv < heads * d || ldo < heads * d || ldq % 8 || ldk % 8 || ldv % 8 || ldo % 8 ||
+        B > 65535 || heads > 65535)
+        return fail(ctx, SDU_ERR_ARG, "bad attention shape");
+    if (!fits(q, (size_t)B * Sq * ldq * 2) || !fits(k, (size_t)B * Sk * ldk * 2) ||
+        !fits(v, (size_t)B * Sk * ldv * 2) || !fits(o, (size_t)B * Sq * ldo * 2))
+        return fail(ctx, SDU_ERR_ARG, "attention tensor too small");
+    AttnArgs a{(const f16*)dptr(q), (const f16*)dptr(k), (const f16*)dptr(v), (f16*)dptr(o), B, heads, Sq, Sk,
+               d, ldq, ldk, ldv, ldo, scale};
+    return finish(ctx, attention_launch(a, ctx->c.stream), "attention");
+}
+
+int sdu_geglu(sdu_ctx* ctx, const sdu_tensor* g, sdu_tensor* y, int T, int C2) {
+    SDU_GUARD(ctx);
+    if (T < 1 || C2 < 1) return fail(ctx, SDU_ERR_ARG, "bad geglu shape");
+    if (!fits(g, (size_t)T * C2 * 4) || !fits(y, (size_t)T * C2 * 2)) return fail(ctx, SDU_ERR_ARG, "geglu tensor too small");
+    return finish(ctx, geglu_launch((const f16*)dptr(g), (f16*)dptr(y), T, C2, ctx->c.stream), "geglu");
+}
+
+int sdu_silu(sdu_ctx* ctx, const sdu_tensor* x, sdu_tensor* y, int64_t n) {
+    SDU_GUARD(ctx);
+    if (n < 0 || !fits(x, (size_t)n * 2) || !fits(y, (size_t)n * 2)) return fail(ctx, SDU_ERR_ARG, "bad silu");
+    if (n == 0) return SDU_OK;
+    return finish(ctx, silu_launch((const f16*)dptr(x), (f16*)dptr(y), n, ctx->c.stream), "silu");
+}
+
+int sdu_add(sdu_ctx* ctx, const sdu_tensor* a, const sdu_tensor* b, sdu_tensor* y, int64_t n) {
+    SDU_GUARD(ctx);
+    if (n < 0 || !fits(a, (size_t)n * 2) || !fits(b, (size_t)n * 2) || !fits(y, (size_t)n * 2))
+        return fail(ctx, SDU_ERR_ARG, "bad add");
+    if (n == 0) return SDU_OK;
+    return finish(ctx, add_launch((const f16*)dptr(a), (const f16*)dptr(b), (f16*)dptr(y), n, ctx->c.stream), "add");
+}
+
+int sdu_add_bias(sdu_ctx* ctx, sdu_tensor* y, const sdu_tensor* bias, int64_t n, int C) {
+    SDU_GUARD(ctx);
+    if (n < 0 || C < 1 || !fits(y, (size_t)n * 2) || !fits(bias, (size_t)C * 2))
+        return fail(ctx, SDU_ERR_ARG, "bad add_bias");
+    if (n == 0) return SDU_OK;
+    return finish(ctx, add_bias_launch((f16*)dptr(y), (const f16*)dptr(bias), n, C, ctx->c.stream), "add_bias");
+}
+
+int sdu_lcm_step(sdu_ctx* ctx, sdu_tensor* x, const sdu_tensor* eps2, const sdu_tensor* noise, int64_t n,
+                 int steps, int idx, float guidance) {
+    SDU_GUARD(ctx);
+    if (n < 1 || steps < 1 || steps > 50 || idx < 0 || idx >= steps) return fail(ctx, SDU_ERR_ARG, "bad lcm step");
+    const bool last = idx == steps - 1;
+    if (!fits(x, (size_t)n * 4) || !fits(eps2, (size_t)2 * n * 4) || (!last && !fits(noise, (size_t)n * 4)))
+        return fail(ctx, SDU_ERR_ARG, "lcm tensor too small");
+    // schedule (LcmScheduler.kt:25-68)
+    const int n_train = 1000, n_orig = 50, k = n_train / n_orig;
+    std::vector<double> ac(n_train);
+    double acc = 1.0;
+    for (int i = 0; i < n_train; ++i) {
+        const double s = std::sqrt(0.00085) + (std::sqrt(0.0120) - std::sqrt(0.00085)) * i / (n_train - 1);
+        acc *= 1.0 - s * s;
+        ac[i] = acc;
+    }
+    auto ts = [&](int j) { return (n_orig - (int)std::floor((double)j * n_orig / steps)) * k - 1; };
+    const int t = ts(idx);
+    const double st = t * 10.0, sd2 = 0.25;
+    LcmCoeffs c{};
+    c.guidance = guidance;
+    c.sqrt_alpha = std::sqrt(ac[t]);
+    c.sqrt_beta = std::sqrt(1.0 - ac[t]);
+    c.c_skip = sd2 / (st * st + sd2);
+    c.c_out = st / std::sqrt(st * st + sd2);
+    c.last = last;
+    const double ap = last ? 1.0 : ac[ts(idx + 1)];
+    c.sqrt_alpha_prev = std::sqrt(ap);
+    c.sqrt_beta_prev = std::sqrt(1.0 - ap);
+    return finish(ctx, lcm_step_launch((float*)dptr(x), (const float*)dptr(eps2), last ? nullptr : (const float*)dptr(noise),
+                                       n, c, nullptr, 0, 1, 1, ctx->c.stream),
+                  "lcm_step");
+}
+
+}  // extern "C"

@@ -1,0 +1,148 @@
+// Host-side engine state shared by runtime.cpp, unet.cpp and capi.cpp.
+#pragma once
+
+#include "sdu_internal.h"
+#include "../../include/sdu.h"
+
+#include <map>
+#include <memory>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+namespace sdu {
+
+enum WKind { WK_CONV = 0, WK_LINEAR = 1, WK_NORM_W = 2, WK_NORM_B = 3, WK_BIAS = 4 };
+
+// One named UNet parameter.  `dev` points into the weight pool; the device layout
+// is described by (layout, ci_pad): conv weights are [Co, kh, kw, Ci_pad] (the
+// K dimension of the implicit GEMM is tap-major, channel-minor), Linear weights
+// [out, in], the GEGLU projection row-interleaved per 32 (a, b).
+struct WeightRec {
+    std::string name;
+    std::vector<int64_t> shape;  // canonical (diffusers) shape
+    int kind = 0;
+    int layout = GL_PLAIN;
+    int ci_pad = 0;
+    f16* dev = nullptr;
+    int64_t dev_n = 0;
+    int64_t numel() const {
+        int64_t n = 1;
+        for (auto s : shape) n *= s;
+        return n;
+    }
+};
+
+// Bump arena with stack marks.  In sizing mode it hands out no memory and only
+// records the high-water mark.
+struct Arena {
+    char* base = nullptr;
+    size_t cap = 0, top = 0, high = 0;
+    bool sizing = false;
+    void* alloc(size_t bytes) {
+        size_t off = (top + 255) & ~(size_t)255;
+        top = off + ((bytes + 255) & ~(size_t)255);
+        if (top > high) high = top;
+        if (sizing) return nullptr;
+        return base + off;
+    }
+    size_t mark() const { return top; }
+    void release(size_t m) { top = m; }
+};
+
+// Shapes of one UNet instance: per-resnet / per-transformer channel counts and
+// offsets into the fused time-projection and cross-K/V weight blocks.
+struct ResDesc {
+    std::string pf;
+    int cin, cout, cin1;  // cin1: channels from the first source (concat split)
+    int tproj_off;
+};
+struct XfDesc {
+    std::string pf;
+    int c;
+    int kv_off;  // column offset of this block's K in the fused cross K/V output
+};
+
+struct ProfAcc {
+    int calls = 0;
+    double ms = 0, flops = 0, bytes = 0;
+};
+
+struct FwdState;  // per-shape graph state (unet.cpp)
+
+struct Ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string err;
+    uint64_t seed = 0;
+    int flags = 0;
+
+    // weights
+    f16* wpool = nullptr;
+    size_t wpool_bytes = 0, wpool_top = 0;
+    std::vector<WeightRec> weights;
+    std::unordered_map<std::string, int> widx;
+    // fused blocks
+    f16* w_tproj = nullptr;   // [sum Cout, 1280]
+    f16* b_tproj = nullptr;   // [sum Cout]
+    int tproj_total = 0;
+    f16* w_kv = nullptr;      // [sum 2C, 768]
+    int kv_total = 0;
+    std::vector<ResDesc> resnets;
+    std::vector<XfDesc> xfs;
+    std::map<std::string, int> res_by_pf, xf_by_pf;
+
+    // op-level tensors and per-shape forward state
+    std::vector<FwdState*> fwd;  // owned; freed by free_fwd_states
+    float* op_ws = nullptr;     // scratch for op-level calls
+    size_t op_ws_bytes = 0;
+
+    // profiling
+    bool profiling = false;
+    std::map<std::string, ProfAcc> prof;
+
+    const WeightRec* w(const std::string& name) const {
+        auto it = widx.find(name);
+        return it == widx.end() ? nullptr : &weights[it->second];
+    }
+    f16* wd(const std::string& name) const {
+        const WeightRec* r = w(name);
+        return r ? r->dev : nullptr;
+    }
+};
+
+struct sdu_tensor_impl {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    int dtype = SDU_F16;
+    std::vector<int64_t> shape;
+};
+
+// runtime.cpp
+int build_inventory(Ctx& c);                       // fills weights / descs and allocates the pool
+int init_weights_seeded(Ctx& c);
+int init_weights_dir(Ctx& c, const std::string& dir);
+int set_weight_canonical(Ctx& c, const WeightRec& r, const float* data);
+int get_weight_canonical(Ctx& c, const WeightRec& r, float* out);
+int ensure_op_ws(Ctx& c, size_t bytes);
+int set_err(Ctx* c, int code, const std::string& msg);
+
+// unet.cpp
+int unet_forward_host(Ctx& c, const float* lat, const float* temb, const float* ctx, int B, int H,
+                      int W, int L, float* out);
+int unet_forward_device(Ctx& c, const float* d_lat, const float* d_temb, const float* d_ctx, int B,
+                        int H, int W, int L, float* d_out);
+int unet_denoise_device(Ctx& c, const float* d_lat, const float* d_cond, const float* d_uncond,
+                        int H, int W, int L, int steps, float guidance, const float* d_noise,
+                        float* d_out);
+int unet_profile(Ctx& c, int B, int H, int W, int L);
+void free_fwd_states(Ctx& c);
+
+}  // namespace sdu
+
+struct sdu_ctx {
+    sdu::Ctx c;
+};
+struct sdu_tensor {
+    sdu::sdu_tensor_impl t;
+};

@@ -1,0 +1,194 @@
+// Layout conversion, elementwise ops, the fused CFG + LCM step, and the seeded
+// weight generator.
+//
+//  * nchw_to_nhwc: the C-ABI edge.  The reference's boundary tensors are fp32
+//    [C, B*HW] / NCHW (vk_engine.cpp:874-913); inside, activations are NHWC fp16.
+//  * silu / add / add_bias / geglu: SILU, ADD, AB2, GEGLU shaders
+//    (silu_f32.comp, add_f32.comp, addbias2_f32.comp, geglu_f32.comp) as
+//    standalone ops of the C ABI.  Inside the UNet graph they are fused into GEMM
+//    epilogues.
+//  * lcm_step: CFG combine (VulkanUnetPipeline.kt:86) + LcmScheduler.step
+//    (LcmScheduler.kt:56-82) in one pass, also writing the next UNet input.
+//  * gen: device side of the seeded generator specified in oracle/gen.c.
+#include "sdu_internal.h"
+
+namespace sdu {
+
+__global__ void nchw_to_nhwc_kernel(const float* src, f16* dst, int B, int Bsrc, int C, int Cpad,
+                                    int HW) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t total = (int64_t)B * HW * Cpad;
+    if (i >= total) return;
+    const int c = (int)(i % Cpad);
+    const int64_t pix = i / Cpad;
+    const int b = (int)(pix / HW), p = (int)(pix % HW);
+    float v = 0.f;
+    if (c < C) v = src[((int64_t)(b % Bsrc) * C + c) * HW + p];
+    dst[i] = (f16)v;
+}
+
+hipError_t nchw_to_nhwc_launch(const float* src, f16* dst, int B, int Bsrc, int C, int Cpad, int HW,
+                               hipStream_t s) {
+    const int64_t total = (int64_t)B * HW * Cpad;
+    hipLaunchKernelGGL(nchw_to_nhwc_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                       src, dst, B, Bsrc, C, Cpad, HW);
+    return hipGetLastError();
+}
+
+__global__ void f32_to_f16_kernel(const float* src, f16* dst, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) dst[i] = (f16)src[i];
+}
+__global__ void f16_to_f32_kernel(const f16* src, float* dst, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) dst[i] = (float)src[i];
+}
+hipError_t f32_to_f16_launch(const float* src, f16* dst, int64_t n, hipStream_t s) {
+    hipLaunchKernelGGL(f32_to_f16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src, dst, n);
+    return hipGetLastError();
+}
+hipError_t f16_to_f32_launch(const f16* src, float* dst, int64_t n, hipStream_t s) {
+    hipLaunchKernelGGL(f16_to_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src, dst, n);
+    return hipGetLastError();
+}
+
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }
+
+// float -> fp16 (round to nearest even) of a value that must first be rounded to
+// float: the empty asm pins the float intermediate, otherwise the compiler folds
+// (f16)(float)double into one double -> half rounding, which differs from the
+// two-step rounding the generator and the scheduler specify.
+__device__ __forceinline__ f16 f16_via_f32(float f) {
+    asm volatile("" : "+v"(f));
+    return (f16)f;
+}
+
+__global__ void silu_kernel(const f16* x, f16* y, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = (f16)silu_f((float)x[i]);
+}
+__global__ void add_kernel(const f16* a, const f16* b, f16* y, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = (f16)((float)a[i] + (float)b[i]);
+}
+__global__ void add_bias_kernel(f16* y, const f16* bias, int64_t n, int C) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = (f16)((float)y[i] + (float)bias[i % C]);
+}
+__global__ void geglu_kernel(const f16* g, f16* y, int T, int C2) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)T * C2) return;
+    const int64_t t = i / C2;
+    const int c = (int)(i - t * C2);
+    const float a = (float)g[t * 2 * C2 + c], bb = (float)g[t * 2 * C2 + C2 + c];
+    y[i] = (f16)(a * (0.5f * bb * (1.0f + erff(bb * 0.70710678118654752f))));
+}
+
+hipError_t silu_launch(const f16* x, f16* y, int64_t n, hipStream_t s) {
+    hipLaunchKernelGGL(silu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, y, n);
+    return hipGetLastError();
+}
+hipError_t add_launch(const f16* a, const f16* b, f16* y, int64_t n, hipStream_t s) {
+    hipLaunchKernelGGL(add_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a, b, y, n);
+    return hipGetLastError();
+}
+hipError_t add_bias_launch(f16* y, const f16* bias, int64_t n, int C, hipStream_t s) {
+    hipLaunchKernelGGL(add_bias_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, y, bias, n, C);
+    return hipGetLastError();
+}
+hipError_t geglu_launch(const f16* g, f16* y, int T, int C2, hipStream_t s) {
+    const int64_t n = (int64_t)T * C2;
+    hipLaunchKernelGGL(geglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, g, y, T, C2);
+    return hipGetLastError();
+}
+
+// ----------------------------------------------------------------- CFG + LCM step
+
+__global__ void lcm_step_kernel(float* x, const float* eps2, const float* noise, int64_t n,
+                                LcmCoeffs c, f16* unet_in, int C, int HW, int Cpad) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    // Every operation rounds separately (no FMA contraction), in the order of the
+    // host formulas, so the device loop reproduces a host loop bit for bit.
+    // eps = u + s (c - u) in float32 (VulkanUnetPipeline.kt:86)
+    const float ec = eps2[i], eu = eps2[n + i];
+    const float eps = __fadd_rn(eu, __fmul_rn(c.guidance, __fsub_rn(ec, eu)));
+    // LcmScheduler.kt:70-79 in float64
+    const double xv = (double)x[i];
+    const double x0 = __ddiv_rn(__dsub_rn(xv, __dmul_rn(c.sqrt_beta, (double)eps)), c.sqrt_alpha);
+    const double den = __dadd_rn(__dmul_rn(c.c_out, x0), __dmul_rn(c.c_skip, xv));
+    float out;
+    if (c.last) out = (float)den;
+    else out = (float)__dadd_rn(__dmul_rn(c.sqrt_alpha_prev, den), __dmul_rn(c.sqrt_beta_prev, (double)noise[i]));
+    x[i] = out;
+    if (unet_in) {
+        // i indexes the NCHW latent [C, HW]; write NHWC [2, HW, Cpad] for both slots
+        const int ch = (int)(i / HW), p = (int)(i % HW);
+        const f16 h = f16_via_f32(out);
+        unet_in[(int64_t)p * Cpad + ch] = h;
+        unet_in[((int64_t)HW + p) * Cpad + ch] = h;
+    }
+}
+
+hipError_t lcm_step_launch(float* x, const float* eps2, const float* noise, int64_t n, LcmCoeffs c,
+                           f16* unet_in, int C, int HW, int Cpad, hipStream_t s) {
+    hipLaunchKernelGGL(lcm_step_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, eps2,
+                       noise, n, c, unet_in, C, HW, Cpad);
+    return hipGetLastError();
+}
+
+// ----------------------------------------------------------------- generator
+
+__host__ __device__ __forceinline__ uint64_t mix64(uint64_t x) {
+    x += 0x9E3779B97F4A7C15ULL;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBULL;
+    return x ^ (x >> 31);
+}
+
+uint64_t splitmix64(uint64_t x) { return mix64(x); }
+
+uint64_t fnv1a64(const char* s) {
+    uint64_t h = 0xCBF29CE484222325ULL;
+    for (; *s; ++s) { h ^= (uint8_t)*s; h *= 0x100000001B3ULL; }
+    return h;
+}
+
+__global__ void gen_kernel(f16* dst, GenDesc g) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= g.n) return;
+    if (g.constant) { dst[i] = f16_via_f32((float)g.mean); return; }
+    int64_t ci;  // canonical index
+    if (g.layout == GL_CONV_OHWI) {
+        // device [co, kh, kw, ci_pad] -> canonical [co, ci, kh, kw]
+        const int c = (int)(i % g.ci_pad);
+        int64_t r = i / g.ci_pad;
+        const int kx = (int)(r % g.kw); r /= g.kw;
+        const int ky = (int)(r % g.kh);
+        const int o = (int)(r / g.kh);
+        if (c >= g.ci) { dst[i] = (f16)0.f; return; }
+        ci = (((int64_t)o * g.ci + c) * g.kh + ky) * g.kw + kx;
+    } else if (g.layout == GL_GEGLU_PERM) {
+        // device row r: 64-row blocks [32 rows of the first half | 32 of the second]
+        const int64_t r = i / g.cols;
+        const int col = (int)(i % g.cols);
+        const int64_t blk = r / 64, w = r % 64;
+        const int64_t cr = (w < 32) ? blk * 32 + w : (int64_t)g.half_rows + blk * 32 + (w - 32);
+        ci = cr * g.cols + col;
+    } else {
+        ci = i;
+    }
+    const uint64_t h1 = mix64(g.key + 2ULL * (uint64_t)ci);
+    const uint64_t h2 = mix64(g.key + 2ULL * (uint64_t)ci + 1ULL);
+    const double u1 = (double)((h1 >> 11) + 1ULL) * 0x1.0p-53;
+    const double u2 = (double)(h2 >> 11) * 0x1.0p-53;
+    const double z = sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
+    dst[i] = f16_via_f32((float)__dadd_rn(g.mean, __dmul_rn(g.stdv, z)));
+}
+
+hipError_t gen_launch(f16* dst, const GenDesc& g, hipStream_t s) {
+    hipLaunchKernelGGL(gen_kernel, dim3((unsigned)((g.n + 255) / 256)), dim3(256), 0, s, dst, g);
+    return hipGetLastError();
+}
+
+}  // namespace sdu

@@ -1,0 +1,123 @@
+// Internal interfaces between the host runtime (runtime.cpp, unet.cpp, capi.cpp)
+// and the gfx950 kernels (k_*.hip).  Not part of the public ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <cstdint>
+#include <cstddef>
+
+namespace sdu {
+
+typedef _Float16 f16;
+
+// ----------------------------------------------------------------- GEMM
+// C[M,N] = A[M,K] . W[N,K]^T with a fused epilogue.  A is either a dense
+// row-major matrix (optionally split over two sources along K) or the implicit
+// im2col of an NHWC image for a 3x3 conv (pad 1, stride 1/2, optional 2x
+// nearest upsample of the input).
+enum AMode { A_DENSE = 0, A_CONV3 = 1 };
+enum OutMode { OUT_F16 = 0, OUT_F32 = 1, OUT_F32_NCHW = 2 };
+
+struct GemmArgs {
+    int M, N, K;
+    // A operand
+    int amode;
+    const f16* A;     // dense: [M, lda]; conv: NHWC input [B, Hin, Win, Cin]
+    int lda;
+    const f16* A2;    // dense only: columns [K1, K) come from A2 [M, lda2]
+    int lda2;
+    int K1;           // dense: split point (K when A2 == nullptr)
+    int Bn, Hin, Win, Cin, Ho, Wo, stride, upsample;  // conv geometry
+    // B operand: W [N, K] row-major
+    const f16* Wt;
+    // epilogue
+    const f16* bias;    // [N] or null
+    const float* bias2; // [N] fp32 or null (time projection broadcast)
+    const f16* res;     // [M, ldr] residual or null
+    int ldr;
+    void* C;            // output
+    int ldc;            // row stride of C in elements (after GEGLU: N/2 columns)
+    int out_mode;
+    int hw_out;         // OUT_F32_NCHW: pixels per image
+    int geglu;
+    // split-K
+    float* partial;     // [splits, M, N] fp32 (null: no split)
+    int splits;
+    int k_per_split;    // multiple of the K tile
+};
+
+// Picks the tile shape and split-K factor; returns the fp32 workspace bytes the
+// launch needs (0 if none).  `ws` may be null when the return value is 0.
+size_t gemm_workspace_bytes(const GemmArgs& a);
+hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s);
+
+// y[n] = act_out( sum_k act_in(x[k]) * W[n,k] + bias[n] ), fp32 in/out, W fp16 [N,K].
+// act: 0 none, 1 SiLU.
+hipError_t gemv_launch(const float* x, const f16* W, const f16* bias, float* y, int N, int K,
+                       int act_in, int act_out, hipStream_t s);
+
+// ----------------------------------------------------------------- attention
+struct AttnArgs {
+    const f16* q; const f16* k; const f16* v; f16* o;
+    int B, heads, Sq, Sk, d;
+    int ldq, ldk, ldv, ldo;
+    float scale;
+};
+hipError_t attention_launch(const AttnArgs& a, hipStream_t s);
+
+// ----------------------------------------------------------------- norms
+// GroupNorm accumulator: fp64 [B][G][2] (sum, sum of squares); must be zero on
+// entry (zero_launch).  C = C1 + C2 <= 2560, G <= 32.
+size_t groupnorm_acc_bytes(int B, int G);
+hipError_t groupnorm_launch(const f16* x, const f16* x2, int C1, int C2, const f16* gamma,
+                            const f16* beta, f16* y, int B, int HW, int G, float eps, int silu,
+                            double* acc, hipStream_t s);
+// Clear `bytes` (rounded up to 16) with a fill kernel (graph-safe, no memset node).
+hipError_t zero_launch(void* p, size_t bytes, hipStream_t s);
+hipError_t layernorm_launch(const f16* x, const f16* gamma, const f16* beta, f16* y, int T, int C,
+                            float eps, hipStream_t s);
+
+// ----------------------------------------------------------------- elementwise
+// NCHW fp32 [Bsrc,C,H,W] -> NHWC fp16 [B,H,W,Cpad]; batch b reads source b % Bsrc,
+// channels >= C are zero.
+hipError_t nchw_to_nhwc_launch(const float* src, f16* dst, int B, int Bsrc, int C, int Cpad, int HW,
+                               hipStream_t s);
+// fp32 -> fp16 copy
+hipError_t f32_to_f16_launch(const float* src, f16* dst, int64_t n, hipStream_t s);
+hipError_t f16_to_f32_launch(const f16* src, float* dst, int64_t n, hipStream_t s);
+hipError_t silu_launch(const f16* x, f16* y, int64_t n, hipStream_t s);
+hipError_t add_launch(const f16* a, const f16* b, f16* y, int64_t n, hipStream_t s);
+hipError_t add_bias_launch(f16* y, const f16* bias, int64_t n, int C, hipStream_t s);
+hipError_t geglu_launch(const f16* g, f16* y, int T, int C2, hipStream_t s);
+
+struct LcmCoeffs {
+    float guidance;
+    double sqrt_alpha, sqrt_beta, c_skip, c_out, sqrt_alpha_prev, sqrt_beta_prev;
+    int last;
+};
+// eps2: [2, n] (cond, uncond) fp32; x: [n] fp32 updated in place; noise [n] or null.
+// If unet_in != null, also writes the next UNet input NHWC fp16 [2, HW, Cpad]
+// (x duplicated into both CFG slots, C channels of HW pixels).
+hipError_t lcm_step_launch(float* x, const float* eps2, const float* noise, int64_t n,
+                           LcmCoeffs c, f16* unet_in, int C, int HW, int Cpad, hipStream_t s);
+
+// Seeded fp16 N(mean, std) generator (same specification as the oracle's gen.c).
+// Layout descriptors map device index -> canonical (diffusers) index.
+enum GenLayout { GL_PLAIN = 0, GL_CONV_OHWI = 1, GL_GEGLU_PERM = 2 };
+struct GenDesc {
+    uint64_t key;
+    int64_t n;         // device elements
+    int layout;
+    int co, ci, kh, kw, ci_pad;  // GL_CONV_OHWI: canonical [co,ci,kh,kw] -> device [co,kh,kw,ci_pad]
+    int half_rows, cols;         // GL_GEGLU_PERM: canonical [2*half_rows, cols]
+    double mean, stdv;
+    int constant;      // 1: fill `mean` (no randomness)
+};
+hipError_t gen_launch(f16* dst, const GenDesc& g, hipStream_t s);
+
+uint64_t fnv1a64(const char* s);
+uint64_t splitmix64(uint64_t x);
+
+}  // namespace sdu

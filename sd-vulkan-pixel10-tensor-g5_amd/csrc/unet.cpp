@@ -1,0 +1,668 @@
+// SD1.5 UNet graph on the HIP kernels: blocks, full forward, LCM denoise loop.
+//
+// Restates runGraph (vk_engine.cpp:711-790) and its blocks (:623-697) over NHWC
+// fp16 activations.  Each forward is planned once per shape: a sizing pass runs
+// the graph without launching to size the activation arena and workspaces, then
+// the real pass is captured into a HIP graph and replayed on later calls (the
+// reference records one command buffer per forward, :714, :783-788).
+#include "engine.h"
+
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+
+namespace sdu {
+
+static const int kGroups = 32;
+static const float kEps = 1e-5f;  // GN and LN (vk_engine.cpp:548-549, :652)
+static const int kHeads = 8;
+static const int kLatC = 4, kLatCpad = 8, kCtxDim = 768;
+
+// ------------------------------------------------------------------ execution
+
+struct ProfRec {
+    std::string cat, kern, shape;
+    double flops, bytes;
+    hipEvent_t e0, e1;
+};
+
+struct Exec {
+    Ctx& c;
+    hipStream_t s;
+    Arena* ar;
+    int B;
+    bool dry = false;
+    float* gemm_ws = nullptr;
+    size_t gemm_ws_need = 0;
+    double* gn_acc = nullptr;  // next free GroupNorm accumulator slot (zeroed per forward)
+    hipError_t err = hipSuccess;
+    std::vector<ProfRec>* prof = nullptr;
+
+    template <class T>
+    T* alloc(size_t n) { return (T*)ar->alloc(n * sizeof(T)); }
+
+    template <class F>
+    void run(const char* cat, const char* kern, double flops, double bytes, F&& launch,
+             const std::string& shape = std::string()) {
+        if (dry || err != hipSuccess) return;
+        ProfRec pr;
+        if (prof) {
+            pr.cat = cat; pr.kern = kern; pr.flops = flops; pr.bytes = bytes; pr.shape = shape;
+            hipEventCreate(&pr.e0);
+            hipEventCreate(&pr.e1);
+            hipEventRecord(pr.e0, s);
+        }
+        hipError_t e = launch();
+        if (e != hipSuccess) err = e;
+        if (prof) {
+            hipEventRecord(pr.e1, s);
+            prof->push_back(pr);
+        }
+    }
+};
+
+static const char* gemm_kernel_name(const GemmArgs& a) {
+    return a.N <= 64 && !a.geglu ? "gemm_128x64" : "gemm_128x128";
+}
+
+static void gemm(Exec& E, const char* cat, const GemmArgs& a, double flops) {
+    const size_t ws = gemm_workspace_bytes(a);
+    if (ws > E.gemm_ws_need) E.gemm_ws_need = ws;
+    const double out_el = (double)a.M * (a.geglu ? a.N / 2 : a.N);
+    const double bytes = 2.0 * ((double)a.M * a.K + (double)a.N * a.K) +
+                         out_el * (a.out_mode == OUT_F16 ? 2.0 : 4.0) + (a.res ? out_el * 2.0 : 0.0);
+    char shape[96];
+    snprintf(shape, sizeof shape, "%s M=%d N=%d K=%d geglu=%d", a.amode == A_CONV3 ? "conv3" : "dense",
+             a.M, a.N, a.K, a.geglu);
+    E.run(cat, gemm_kernel_name(a), flops, bytes, [&] { return gemm_launch(a, E.gemm_ws, E.s); }, shape);
+}
+
+static GemmArgs dense_args(const f16* A, int lda, int M, int N, int K, const f16* W, void* C, int ldc) {
+    GemmArgs a{};
+    a.M = M; a.N = N; a.K = K;
+    a.amode = A_DENSE;
+    a.A = A; a.lda = lda; a.K1 = K;
+    a.Wt = W;
+    a.C = C; a.ldc = ldc;
+    a.out_mode = OUT_F16;
+    return a;
+}
+
+// 3x3 conv (pad 1) as implicit GEMM; returns output spatial size via Ho/Wo.
+static GemmArgs conv3_args(const f16* x, int B, int Hin, int Win, int Cin, int Cout, int stride,
+                           int ups, const f16* W, void* y) {
+    GemmArgs a{};
+    a.amode = A_CONV3;
+    a.A = x;
+    a.Bn = B; a.Hin = Hin; a.Win = Win; a.Cin = Cin;
+    a.stride = stride; a.upsample = ups;
+    a.Ho = ups ? 2 * Hin : (stride == 2 ? (Hin - 1) / 2 + 1 : Hin);
+    a.Wo = ups ? 2 * Win : (stride == 2 ? (Win - 1) / 2 + 1 : Win);
+    a.M = B * a.Ho * a.Wo; a.N = Cout; a.K = 9 * Cin;
+    a.Wt = W;
+    a.C = y; a.ldc = Cout;
+    a.out_mode = OUT_F16;
+    return a;
+}
+
+static void groupnorm(Exec& E, const f16* x, const f16* x2, int C1, int C2, const f16* g,
+                      const f16* b, f16* y, int HW, int silu) {
+    double* acc = E.gn_acc;
+    E.gn_acc += (size_t)E.B * kGroups * 2;
+    const double bytes = 4.0 * E.B * HW * (C1 + C2);
+    char shape[48];
+    snprintf(shape, sizeof shape, "HW=%d C=%d", HW, C1 + C2);
+    E.run(silu ? "groupnorm_silu" : "groupnorm", "groupnorm", 0, bytes, [&] {
+        return groupnorm_launch(x, x2, C1, C2, g, b, y, E.B, HW, kGroups, kEps, silu, acc, E.s);
+    }, shape);
+}
+
+static void layernorm(Exec& E, const f16* x, const f16* g, const f16* b, f16* y, int T, int C) {
+    E.run("layernorm", "layernorm", 0, 4.0 * T * C,
+          [&] { return layernorm_launch(x, g, b, y, T, C, kEps, E.s); });
+}
+
+static void attention(Exec& E, const char* cat, const f16* q, const f16* k, const f16* v, f16* o,
+                      int Sq, int Sk, int C, int ldq, int ldk, int ldv) {
+    AttnArgs a{q, k, v, o, E.B, kHeads, Sq, Sk, C / kHeads, ldq, ldk, ldv, C,
+               1.0f / sqrtf((float)(C / kHeads))};
+    const double flops = 4.0 * E.B * kHeads * (double)Sq * Sk * (C / kHeads);
+    const double bytes = 2.0 * E.B * ((double)Sq * C * 2 + (double)Sk * C * 2);
+    char kern[32];
+    snprintf(kern, sizeof kern, "attn_d%d", C / kHeads);
+    char shape[64];
+    snprintf(shape, sizeof shape, "Sq=%d Sk=%d d=%d", Sq, Sk, C / kHeads);
+    E.run(cat, kern, flops, bytes, [&] { return attention_launch(a, E.s); }, shape);
+}
+
+// ------------------------------------------------------------------ blocks
+
+struct Fwd {
+    int B, H, W, L;
+};
+
+static const f16* W(Exec& E, const std::string& n) { return E.c.wd(n); }
+
+// ResNet block (vk_engine.cpp:623-637).  x2 != null: input is concat(x, x2).
+static f16* resnet(Exec& E, const ResDesc& r, const f16* x, const f16* x2, int H, int Wd,
+                   const float* tproj) {
+    const int B = E.B, M = B * H * Wd, HW = H * Wd;
+    f16* out = E.alloc<f16>((size_t)M * r.cout);
+    const size_t mk = E.ar->mark();
+    f16* h = E.alloc<f16>((size_t)M * r.cin);
+    groupnorm(E, x, x2, r.cin1, r.cin - r.cin1, W(E, r.pf + ".norm1.weight"), W(E, r.pf + ".norm1.bias"),
+              h, HW, 1);
+    f16* hc = E.alloc<f16>((size_t)M * r.cout);
+    {
+        GemmArgs a = conv3_args(h, B, H, Wd, r.cin, r.cout, 1, 0, W(E, r.pf + ".conv1.weight"), hc);
+        a.bias = W(E, r.pf + ".conv1.bias");
+        a.bias2 = tproj + r.tproj_off;  // + time_emb_proj(silu(temb)) broadcast (:627-630)
+        gemm(E, "conv3x3", a, 2.0 * M * r.cout * 9.0 * r.cin);
+    }
+    f16* h2 = E.alloc<f16>((size_t)M * r.cout);
+    groupnorm(E, hc, nullptr, r.cout, 0, W(E, r.pf + ".norm2.weight"), W(E, r.pf + ".norm2.bias"), h2,
+              HW, 1);
+    const f16* res = x;
+    if (r.cin != r.cout) {  // 1x1 shortcut over (possibly concatenated) input (:634)
+        f16* sx = E.alloc<f16>((size_t)M * r.cout);
+        GemmArgs a = dense_args(x, r.cin1, M, r.cout, r.cin, W(E, r.pf + ".conv_shortcut.weight"), sx, r.cout);
+        if (x2) { a.A2 = x2; a.lda2 = r.cin - r.cin1; a.K1 = r.cin1; }
+        a.bias = W(E, r.pf + ".conv_shortcut.bias");
+        gemm(E, "conv1x1", a, 2.0 * M * r.cout * r.cin);
+        res = sx;
+    }
+    {
+        GemmArgs a = conv3_args(h2, B, H, Wd, r.cout, r.cout, 1, 0, W(E, r.pf + ".conv2.weight"), out);
+        a.bias = W(E, r.pf + ".conv2.bias");
+        a.res = res; a.ldr = r.cout;
+        gemm(E, "conv3x3", a, 2.0 * M * r.cout * 9.0 * r.cout);
+    }
+    E.ar->release(mk);
+    return out;
+}
+
+// Spatial transformer (vk_engine.cpp:640-675).  kv: fused cross K/V [B*L, kv_total].
+static f16* transformer(Exec& E, const XfDesc& t, const f16* x, int H, int Wd, const f16* kv, int L) {
+    const int B = E.B, HW = H * Wd, M = B * HW, C = t.c;
+    const std::string b = t.pf + ".transformer_blocks.0";
+    f16* out = E.alloc<f16>((size_t)M * C);
+    const size_t mk = E.ar->mark();
+    f16* g = E.alloc<f16>((size_t)M * C);
+    groupnorm(E, x, nullptr, C, 0, W(E, t.pf + ".norm.weight"), W(E, t.pf + ".norm.bias"), g, HW, 0);
+    f16* tt = E.alloc<f16>((size_t)M * C);  // token stream [B*HW, C] (no T_CH transpose: NHWC)
+    {
+        GemmArgs a = dense_args(g, C, M, C, C, W(E, t.pf + ".proj_in.weight"), tt, C);
+        a.bias = W(E, t.pf + ".proj_in.bias");
+        gemm(E, "conv1x1", a, 2.0 * M * C * C);
+    }
+    f16* h = E.alloc<f16>((size_t)M * C);
+    f16* qkv = E.alloc<f16>((size_t)M * 3 * C);
+    f16* at = E.alloc<f16>((size_t)M * C);
+    // self-attention
+    layernorm(E, tt, W(E, b + ".norm1.weight"), W(E, b + ".norm1.bias"), h, M, C);
+    gemm(E, "linear", dense_args(h, C, M, 3 * C, C, W(E, b + ".attn1.to_q.weight"), qkv, 3 * C),
+         2.0 * M * 3 * C * C);
+    attention(E, "attn_self", qkv, qkv + C, qkv + 2 * C, at, HW, HW, C, 3 * C, 3 * C, 3 * C);
+    {
+        GemmArgs a = dense_args(at, C, M, C, C, W(E, b + ".attn1.to_out.0.weight"), tt, C);
+        a.bias = W(E, b + ".attn1.to_out.0.bias");
+        a.res = tt; a.ldr = C;
+        gemm(E, "linear", a, 2.0 * M * C * C);
+    }
+    // cross-attention: K/V of this block are columns [kv_off, kv_off + 2C) of kv
+    layernorm(E, tt, W(E, b + ".norm2.weight"), W(E, b + ".norm2.bias"), h, M, C);
+    gemm(E, "linear", dense_args(h, C, M, C, C, W(E, b + ".attn2.to_q.weight"), qkv, C), 2.0 * M * C * C);
+    const int ldkv = E.c.kv_total;
+    attention(E, "attn_cross", qkv, kv + t.kv_off, kv + t.kv_off + C, at, HW, L, C, C, ldkv, ldkv);
+    {
+        GemmArgs a = dense_args(at, C, M, C, C, W(E, b + ".attn2.to_out.0.weight"), tt, C);
+        a.bias = W(E, b + ".attn2.to_out.0.bias");
+        a.res = tt; a.ldr = C;
+        gemm(E, "linear", a, 2.0 * M * C * C);
+    }
+    // GEGLU feed-forward: proj (+bias, GEGLU in the epilogue) then out (+bias, +residual)
+    layernorm(E, tt, W(E, b + ".norm3.weight"), W(E, b + ".norm3.bias"), h, M, C);
+    f16* ff = E.alloc<f16>((size_t)M * 4 * C);
+    {
+        GemmArgs a = dense_args(h, C, M, 8 * C, C, W(E, b + ".ff.net.0.proj.weight"), ff, 4 * C);
+        a.bias = W(E, b + ".ff.net.0.proj.bias");
+        a.geglu = 1;
+        gemm(E, "linear_geglu", a, 2.0 * M * 8 * C * C);
+    }
+    {
+        GemmArgs a = dense_args(ff, 4 * C, M, C, 4 * C, W(E, b + ".ff.net.2.weight"), tt, C);
+        a.bias = W(E, b + ".ff.net.2.bias");
+        a.res = tt; a.ldr = C;
+        gemm(E, "linear", a, 2.0 * M * C * 4 * C);
+    }
+    {
+        GemmArgs a = dense_args(tt, C, M, C, C, W(E, t.pf + ".proj_out.weight"), out, C);
+        a.bias = W(E, t.pf + ".proj_out.bias");
+        a.res = x; a.ldr = C;
+        gemm(E, "conv1x1", a, 2.0 * M * C * C);
+    }
+    E.ar->release(mk);
+    return out;
+}
+
+static f16* conv3_block(Exec& E, const std::string& pf, const f16* x, int H, int Wd, int Cin, int Cout,
+                        int stride, int ups) {
+    GemmArgs a = conv3_args(x, E.B, H, Wd, Cin, Cout, stride, ups, W(E, pf + ".weight"), nullptr);
+    f16* y = E.alloc<f16>((size_t)a.M * Cout);
+    a.C = y;
+    a.bias = W(E, pf + ".bias");
+    gemm(E, "conv3x3", a, 2.0 * a.M * Cout * 9.0 * Cin);
+    return y;
+}
+
+// time MLP (vk_engine.cpp:716-717) + every resnet's time_emb_proj(silu(temb)) in
+// one GEMV over the fused projection block.  Returns tproj [tproj_total] fp32.
+static float* time_embed(Exec& E, const float* temb320) {
+    Ctx& c = E.c;
+    float* t1 = E.alloc<float>(1280);
+    float* temb = E.alloc<float>(1280);
+    float* tproj = E.alloc<float>(c.tproj_total);
+    E.run("time_mlp", "gemv", 2.0 * 1280 * 320, 2.0 * 1280 * 320, [&] {
+        return gemv_launch(temb320, c.wd("time_embedding.linear_1.weight"), c.wd("time_embedding.linear_1.bias"),
+                           t1, 1280, 320, 0, 1, E.s);
+    });
+    E.run("time_mlp", "gemv", 2.0 * 1280 * 1280, 2.0 * 1280 * 1280, [&] {
+        return gemv_launch(t1, c.wd("time_embedding.linear_2.weight"), c.wd("time_embedding.linear_2.bias"),
+                           temb, 1280, 1280, 0, 0, E.s);
+    });
+    E.run("time_mlp", "gemv", 2.0 * c.tproj_total * 1280, 2.0 * c.tproj_total * 1280, [&] {
+        return gemv_launch(temb, c.w_tproj, c.b_tproj, tproj, c.tproj_total, 1280, 1, 0, E.s);
+    });
+    return tproj;
+}
+
+// All 16 transformers' attn2 to_k / to_v in one GEMM: [B*L, 768] x [kv_total, 768]^T.
+static f16* cross_kv(Exec& E, const f16* ctx16, int L) {
+    Ctx& c = E.c;
+    const int M = E.B * L;
+    f16* kv = E.alloc<f16>((size_t)M * c.kv_total);
+    gemm(E, "cross_kv", dense_args(ctx16, kCtxDim, M, c.kv_total, kCtxDim, c.w_kv, kv, c.kv_total),
+         2.0 * M * c.kv_total * kCtxDim);
+    return kv;
+}
+
+// UNet body: lat NHWC fp16 [B,H,W,8] -> eps fp32 NCHW [B,4,H,W] (vk_engine.cpp:711-790).
+static void unet_core(Exec& E, const Fwd& F, const f16* lat, const float* temb320, const f16* kv,
+                      float* out) {
+    Ctx& c = E.c;
+    const size_t mk0 = E.ar->mark();
+    // GroupNorm accumulators of this forward: 2 per resnet, 1 per transformer, conv_norm_out
+    const size_t n_gn = 2 * c.resnets.size() + c.xfs.size() + 1;
+    const size_t acc_bytes = n_gn * groupnorm_acc_bytes(E.B, kGroups);
+    E.gn_acc = E.alloc<double>(acc_bytes / sizeof(double));
+    {
+        void* p = E.gn_acc;
+        E.run("groupnorm", "zero", 0, (double)acc_bytes, [&] { return zero_launch(p, acc_bytes, E.s); });
+    }
+    const float* tproj = time_embed(E, temb320);
+    int H = F.H, Wd = F.W;
+    struct Skip { const f16* p; int ch; };
+    std::vector<Skip> skips;
+    const f16* x = conv3_block(E, "conv_in", lat, H, Wd, kLatCpad, 320, 1, 0);
+    skips.push_back({x, 320});
+    static const int bo[4] = {320, 640, 1280, 1280};
+    static const int uo[4] = {1280, 1280, 640, 320};
+    char pf[96];
+    int cprev = 320;
+    for (int i = 0; i < 4; ++i) {
+        for (int r = 0; r < 2; ++r) {
+            snprintf(pf, sizeof pf, "down_blocks.%d.resnets.%d", i, r);
+            x = resnet(E, c.resnets[c.res_by_pf[pf]], x, nullptr, H, Wd, tproj);
+            if (i < 3) {
+                snprintf(pf, sizeof pf, "down_blocks.%d.attentions.%d", i, r);
+                x = transformer(E, c.xfs[c.xf_by_pf[pf]], x, H, Wd, kv, F.L);
+            }
+            skips.push_back({x, bo[i]});
+        }
+        cprev = bo[i];
+        if (i < 3) {
+            snprintf(pf, sizeof pf, "down_blocks.%d.downsamplers.0.conv", i);
+            x = conv3_block(E, pf, x, H, Wd, bo[i], bo[i], 2, 0);
+            H /= 2; Wd /= 2;
+            skips.push_back({x, bo[i]});
+        }
+    }
+    x = resnet(E, c.resnets[c.res_by_pf["mid_block.resnets.0"]], x, nullptr, H, Wd, tproj);
+    x = transformer(E, c.xfs[c.xf_by_pf["mid_block.attentions.0"]], x, H, Wd, kv, F.L);
+    x = resnet(E, c.resnets[c.res_by_pf["mid_block.resnets.1"]], x, nullptr, H, Wd, tproj);
+    for (int i = 0; i < 4; ++i) {
+        for (int r = 0; r < 3; ++r) {
+            const Skip sk = skips.back();
+            skips.pop_back();
+            snprintf(pf, sizeof pf, "up_blocks.%d.resnets.%d", i, r);
+            const ResDesc& rd = c.resnets[c.res_by_pf[pf]];
+            x = resnet(E, rd, x, sk.p, H, Wd, tproj);  // concat(prev, skip) read in place
+            cprev = uo[i];
+            if (i > 0) {
+                snprintf(pf, sizeof pf, "up_blocks.%d.attentions.%d", i, r);
+                x = transformer(E, c.xfs[c.xf_by_pf[pf]], x, H, Wd, kv, F.L);
+            }
+        }
+        if (i < 3) {
+            snprintf(pf, sizeof pf, "up_blocks.%d.upsamplers.0.conv", i);
+            x = conv3_block(E, pf, x, H, Wd, uo[i], uo[i], 1, 1);
+            H *= 2; Wd *= 2;
+        }
+    }
+    (void)cprev;
+    const int M = E.B * H * Wd;
+    f16* gn = E.alloc<f16>((size_t)M * 320);
+    groupnorm(E, x, nullptr, 320, 0, c.wd("conv_norm_out.weight"), c.wd("conv_norm_out.bias"), gn, H * Wd, 1);
+    GemmArgs a = conv3_args(gn, E.B, H, Wd, 320, kLatC, 1, 0, c.wd("conv_out.weight"), out);
+    a.bias = c.wd("conv_out.bias");
+    a.out_mode = OUT_F32_NCHW;
+    a.ldc = kLatC;
+    a.hw_out = H * Wd;
+    gemm(E, "conv3x3", a, 2.0 * M * kLatC * 9.0 * 320);
+    E.ar->release(mk0);
+}
+
+// ------------------------------------------------------------------ LCM schedule
+
+struct LcmSched {
+    std::vector<int> timesteps;
+    std::vector<double> ac;
+    // LcmScheduler.kt:25-46
+    explicit LcmSched(int steps) {
+        const int n_train = 1000, n_orig = 50;
+        ac.resize(n_train);
+        double acc = 1.0;
+        const double b0 = 0.00085, b1 = 0.0120;
+        for (int i = 0; i < n_train; ++i) {
+            const double s = std::sqrt(b0) + (std::sqrt(b1) - std::sqrt(b0)) * i / (n_train - 1);
+            acc *= 1.0 - s * s;
+            ac[i] = acc;
+        }
+        const int k = n_train / n_orig;
+        std::vector<int> rev(n_orig);
+        for (int j = 0; j < n_orig; ++j) rev[j] = (n_orig - j) * k - 1;
+        for (int j = 0; j < steps; ++j) timesteps.push_back(rev[(int)std::floor((double)j * n_orig / steps)]);
+    }
+    // LcmScheduler.kt:57-68
+    LcmCoeffs coeffs(int idx, float guidance) const {
+        const int steps = (int)timesteps.size();
+        const int t = timesteps[idx];
+        const double a_t = ac[t], st = t * 10.0, sd2 = 0.25;
+        LcmCoeffs c{};
+        c.guidance = guidance;
+        c.sqrt_alpha = std::sqrt(a_t);
+        c.sqrt_beta = std::sqrt(1.0 - a_t);
+        c.c_skip = sd2 / (st * st + sd2);
+        c.c_out = st / std::sqrt(st * st + sd2);
+        c.last = idx == steps - 1;
+        const double ap = c.last ? 1.0 : ac[timesteps[idx + 1]];
+        c.sqrt_alpha_prev = std::sqrt(ap);
+        c.sqrt_beta_prev = std::sqrt(1.0 - ap);
+        return c;
+    }
+};
+
+// sinusoid of VulkanUnetPipeline.kt:36-46 in float64
+static void time_proj_host(int t, float* out) {
+    for (int i = 0; i < 160; ++i) {
+        const double a = t * std::exp(-std::log(10000.0) * i / 160.0);
+        out[i] = (float)std::cos(a);
+        out[160 + i] = (float)std::sin(a);
+    }
+}
+
+// ------------------------------------------------------------------ planned state
+
+struct FwdState {
+    int kind;  // 0 forward, 1 denoise
+    Fwd f;
+    int steps = 0;
+    float guidance = 0.f;
+    char* arena = nullptr;
+    size_t arena_bytes = 0;
+    float* gemm_ws = nullptr;
+    float* in_lat = nullptr;   // forward: [B,4,H,W]; denoise: [4,H,W]
+    float* in_temb = nullptr;  // forward: [320]; denoise: [steps, 320]
+    float* in_ctx = nullptr;   // [B, L, 768]
+    float* in_noise = nullptr; // denoise: [steps-1, 4, H, W]
+    float* out = nullptr;      // forward: [B,4,H,W]; denoise: [4,H,W]
+    hipGraphExec_t exec = nullptr;
+};
+
+static void body(Exec& E, FwdState& S) {
+    const Fwd& F = S.f;
+    const int HW = F.H * F.W;
+    if (S.kind == 0) {
+        f16* lat = E.alloc<f16>((size_t)F.B * HW * kLatCpad);
+        f16* ctx16 = E.alloc<f16>((size_t)F.B * F.L * kCtxDim);
+        E.run("io", "convert", 0, 0, [&] { return nchw_to_nhwc_launch(S.in_lat, lat, F.B, F.B, kLatC, kLatCpad, HW, E.s); });
+        E.run("io", "convert", 0, 0, [&] { return f32_to_f16_launch(S.in_ctx, ctx16, (int64_t)F.B * F.L * kCtxDim, E.s); });
+        const f16* kv = cross_kv(E, ctx16, F.L);
+        unet_core(E, F, lat, S.in_temb, kv, S.out);
+        return;
+    }
+    // denoise: x (fp32 [4,H,W]) lives in `out`; B = 2 (cond, uncond)
+    const int64_t n = (int64_t)kLatC * HW;
+    f16* lat = E.alloc<f16>((size_t)2 * HW * kLatCpad);
+    f16* ctx16 = E.alloc<f16>((size_t)2 * F.L * kCtxDim);
+    float* eps2 = E.alloc<float>((size_t)2 * n);
+    E.run("io", "convert", 0, 0, [&] {
+        hipError_t e = hipMemcpyAsync(S.out, S.in_lat, n * sizeof(float), hipMemcpyDeviceToDevice, E.s);
+        if (e != hipSuccess) return e;
+        return nchw_to_nhwc_launch(S.in_lat, lat, 2, 1, kLatC, kLatCpad, HW, E.s);
+    });
+    E.run("io", "convert", 0, 0, [&] { return f32_to_f16_launch(S.in_ctx, ctx16, (int64_t)2 * F.L * kCtxDim, E.s); });
+    const f16* kv = cross_kv(E, ctx16, F.L);  // context is fixed across steps
+    LcmSched sched(S.steps);
+    for (int i = 0; i < S.steps; ++i) {
+        unet_core(E, F, lat, S.in_temb + (size_t)i * 320, kv, eps2);
+        const LcmCoeffs co = sched.coeffs(i, S.guidance);
+        const float* nz = co.last ? nullptr : S.in_noise + (size_t)i * n;
+        f16* next = co.last ? nullptr : lat;
+        E.run("lcm_step", "lcm_step", 0, 4.0 * n * 5, [&] {
+            return lcm_step_launch(S.out, eps2, nz, n, co, next, kLatC, HW, kLatCpad, E.s);
+        });
+    }
+}
+
+static void free_state(FwdState* S) {
+    if (!S) return;
+    if (S->exec) hipGraphExecDestroy(S->exec);
+    hipFree(S->arena);
+    hipFree(S->gemm_ws);
+    hipFree(S->in_lat);
+    hipFree(S->in_temb);
+    hipFree(S->in_ctx);
+    hipFree(S->in_noise);
+    hipFree(S->out);
+}
+
+void free_fwd_states(Ctx& c) {
+    for (FwdState* s : c.fwd) {
+        free_state(s);
+        delete s;
+    }
+    c.fwd.clear();
+}
+
+static int hip_fail(Ctx& c, hipError_t e, const char* what) {
+    return set_err(&c, SDU_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// Plan a state: size (dry run), allocate, and capture the graph.
+static int plan_state(Ctx& c, FwdState& S) {
+    const int B = S.kind == 0 ? S.f.B : 2;
+    const int HW = S.f.H * S.f.W;
+    Arena ar;
+    ar.sizing = true;
+    Exec dry{c, c.stream, &ar, B};
+    dry.dry = true;
+    body(dry, S);
+    S.arena_bytes = ar.high;
+    auto mal = [&](void** p, size_t bytes) { return hipMalloc(p, bytes < 256 ? 256 : bytes); };
+    hipError_t e;
+    if ((e = mal((void**)&S.arena, S.arena_bytes)) != hipSuccess) return set_err(&c, SDU_ERR_OOM, "arena allocation failed");
+    if ((e = mal((void**)&S.gemm_ws, dry.gemm_ws_need)) != hipSuccess) return set_err(&c, SDU_ERR_OOM, "gemm workspace");
+    const size_t lat_n = (size_t)(S.kind == 0 ? B : 1) * kLatC * HW;
+    if ((e = mal((void**)&S.in_lat, lat_n * 4)) != hipSuccess) return set_err(&c, SDU_ERR_OOM, "staging");
+    if ((e = mal((void**)&S.in_temb, (size_t)(S.kind == 0 ? 1 : S.steps) * 320 * 4)) != hipSuccess) return set_err(&c, SDU_ERR_OOM, "staging");
+    if ((e = mal((void**)&S.in_ctx, (size_t)B * S.f.L * kCtxDim * 4)) != hipSuccess) return set_err(&c, SDU_ERR_OOM, "staging");
+    if (S.kind == 1 && (e = mal((void**)&S.in_noise, (size_t)(S.steps > 1 ? S.steps - 1 : 1) * kLatC * HW * 4)) != hipSuccess)
+        return set_err(&c, SDU_ERR_OOM, "staging");
+    if ((e = mal((void**)&S.out, lat_n * 4)) != hipSuccess) return set_err(&c, SDU_ERR_OOM, "staging");
+    if (S.kind == 1) {
+        LcmSched sched(S.steps);
+        std::vector<float> te((size_t)S.steps * 320);
+        for (int i = 0; i < S.steps; ++i) time_proj_host(sched.timesteps[i], te.data() + (size_t)i * 320);
+        if ((e = hipMemcpy(S.in_temb, te.data(), te.size() * 4, hipMemcpyHostToDevice)) != hipSuccess)
+            return hip_fail(c, e, "temb upload");
+    }
+    // capture
+    ar.sizing = false;
+    ar.base = S.arena;
+    ar.cap = S.arena_bytes;
+    ar.top = ar.high = 0;
+    Exec E{c, c.stream, &ar, B};
+    E.gemm_ws = S.gemm_ws;
+    hipGraph_t g = nullptr;
+    if ((e = hipStreamBeginCapture(c.stream, hipStreamCaptureModeThreadLocal)) != hipSuccess)
+        return hip_fail(c, e, "begin capture");
+    body(E, S);
+    hipError_t ec = hipStreamEndCapture(c.stream, &g);
+    if (E.err != hipSuccess) { if (g) hipGraphDestroy(g); return hip_fail(c, E.err, "kernel launch during capture"); }
+    if (ec != hipSuccess) return hip_fail(c, ec, "end capture");
+    e = hipGraphInstantiate(&S.exec, g, nullptr, nullptr, 0);
+    hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_fail(c, e, "graph instantiate");
+    return SDU_OK;
+}
+
+static FwdState* get_state(Ctx& c, int kind, int B, int H, int W, int L, int steps, float guidance, int* st) {
+    for (FwdState* s : c.fwd)
+        if (s->kind == kind && s->f.B == B && s->f.H == H && s->f.W == W && s->f.L == L &&
+            s->steps == steps && (kind == 0 || s->guidance == guidance))
+            return s;
+    std::unique_ptr<FwdState> S(new FwdState());
+    S->kind = kind;
+    S->f = Fwd{B, H, W, L};
+    S->steps = steps;
+    S->guidance = guidance;
+    *st = plan_state(c, *S);
+    if (*st) { free_state(S.get()); return nullptr; }
+    c.fwd.push_back(S.release());
+    return c.fwd.back();
+}
+
+static int check_shape(Ctx& c, int B, int H, int W, int L) {
+    if (B < 1 || B > 64 || H < 8 || W < 8 || H % 8 || W % 8 || L < 1 || L > 256 || (int64_t)H * W > 65536)
+        return set_err(&c, SDU_ERR_ARG, "unsupported shape (B in 1..64, H/W multiples of 8, L in 1..256)");
+    if (!c.wpool) return set_err(&c, SDU_ERR_WEIGHT, "context has no UNet weights (SDU_INIT_NO_WEIGHTS)");
+    return SDU_OK;
+}
+
+int unet_forward_device(Ctx& c, const float* d_lat, const float* d_temb, const float* d_ctx, int B, int H,
+                        int W, int L, float* d_out) {
+    int st = check_shape(c, B, H, W, L);
+    if (st) return st;
+    FwdState* S = get_state(c, 0, B, H, W, L, 0, 0.f, &st);
+    if (!S) return st;
+    const size_t lat_b = (size_t)B * kLatC * H * W * 4;
+    hipError_t e;
+    if ((e = hipMemcpyAsync(S->in_lat, d_lat, lat_b, hipMemcpyDeviceToDevice, c.stream)) ||
+        (e = hipMemcpyAsync(S->in_temb, d_temb, 320 * 4, hipMemcpyDeviceToDevice, c.stream)) ||
+        (e = hipMemcpyAsync(S->in_ctx, d_ctx, (size_t)B * L * kCtxDim * 4, hipMemcpyDeviceToDevice, c.stream)) ||
+        (e = hipGraphLaunch(S->exec, c.stream)) ||
+        (e = hipMemcpyAsync(d_out, S->out, lat_b, hipMemcpyDeviceToDevice, c.stream)))
+        return hip_fail(c, e, "forward");
+    return SDU_OK;
+}
+
+int unet_forward_host(Ctx& c, const float* lat, const float* temb, const float* ctx, int B, int H, int W,
+                      int L, float* out) {
+    int st = check_shape(c, B, H, W, L);
+    if (st) return st;
+    FwdState* S = get_state(c, 0, B, H, W, L, 0, 0.f, &st);
+    if (!S) return st;
+    const size_t lat_b = (size_t)B * kLatC * H * W * 4;
+    hipError_t e;
+    if ((e = hipMemcpyAsync(S->in_lat, lat, lat_b, hipMemcpyHostToDevice, c.stream)) ||
+        (e = hipMemcpyAsync(S->in_temb, temb, 320 * 4, hipMemcpyHostToDevice, c.stream)) ||
+        (e = hipMemcpyAsync(S->in_ctx, ctx, (size_t)B * L * kCtxDim * 4, hipMemcpyHostToDevice, c.stream)) ||
+        (e = hipGraphLaunch(S->exec, c.stream)) ||
+        (e = hipMemcpyAsync(out, S->out, lat_b, hipMemcpyDeviceToHost, c.stream)) ||
+        (e = hipStreamSynchronize(c.stream)))
+        return hip_fail(c, e, "forward");
+    return SDU_OK;
+}
+
+int unet_denoise_device(Ctx& c, const float* d_lat, const float* d_cond, const float* d_uncond, int H,
+                        int W, int L, int steps, float guidance, const float* d_noise, float* d_out) {
+    int st = check_shape(c, 2, H, W, L);
+    if (st) return st;
+    if (steps < 1 || steps > 50) return set_err(&c, SDU_ERR_ARG, "steps must be in 1..50");
+    if (steps > 1 && !d_noise) return set_err(&c, SDU_ERR_ARG, "noise is required when steps > 1");
+    FwdState* S = get_state(c, 1, 2, H, W, L, steps, guidance, &st);
+    if (!S) return st;
+    const size_t n = (size_t)kLatC * H * W;
+    const size_t cb = (size_t)L * kCtxDim * 4;
+    hipError_t e;
+    if ((e = hipMemcpyAsync(S->in_lat, d_lat, n * 4, hipMemcpyDeviceToDevice, c.stream)) ||
+        (e = hipMemcpyAsync(S->in_ctx, d_cond, cb, hipMemcpyDeviceToDevice, c.stream)) ||
+        (e = hipMemcpyAsync((char*)S->in_ctx + cb, d_uncond, cb, hipMemcpyDeviceToDevice, c.stream)))
+        return hip_fail(c, e, "denoise");
+    if (steps > 1 && (e = hipMemcpyAsync(S->in_noise, d_noise, (size_t)(steps - 1) * n * 4,
+                                         hipMemcpyDeviceToDevice, c.stream)))
+        return hip_fail(c, e, "denoise");
+    if ((e = hipGraphLaunch(S->exec, c.stream)) ||
+        (e = hipMemcpyAsync(d_out, S->out, n * 4, hipMemcpyDeviceToDevice, c.stream)))
+        return hip_fail(c, e, "denoise");
+    return SDU_OK;
+}
+
+// Eager forward with per-kernel HIP events (unetProfile, vk_engine.cpp:854-872).
+int unet_profile(Ctx& c, int B, int H, int W, int L) {
+    int st = check_shape(c, B, H, W, L);
+    if (st) return st;
+    FwdState* S = get_state(c, 0, B, H, W, L, 0, 0.f, &st);
+    if (!S) return st;
+    hipError_t e = hipStreamSynchronize(c.stream);
+    if (e != hipSuccess) return hip_fail(c, e, "profile");
+    Arena ar;
+    ar.base = S->arena;
+    ar.cap = S->arena_bytes;
+    std::vector<ProfRec> recs;
+    Exec E{c, c.stream, &ar, B};
+    E.gemm_ws = S->gemm_ws;
+    E.prof = &recs;
+    body(E, *S);
+    e = hipStreamSynchronize(c.stream);
+    if (E.err != hipSuccess) e = E.err;
+    c.prof.clear();
+    // SDU_PROFILE_DUMP=<path>: also write one CSV line per launch
+    FILE* dump = nullptr;
+    if (const char* path = getenv("SDU_PROFILE_DUMP")) {
+        dump = fopen(path, "w");
+        if (dump) fprintf(dump, "category,kernel,shape,flops,bytes,ms\n");
+    }
+    for (ProfRec& r : recs) {
+        float ms = 0.f;
+        if (e == hipSuccess) hipEventElapsedTime(&ms, r.e0, r.e1);
+        hipEventDestroy(r.e0);
+        hipEventDestroy(r.e1);
+        if (dump) fprintf(dump, "%s,%s,%s,%.0f,%.0f,%.5f\n", r.cat.c_str(), r.kern.c_str(), r.shape.c_str(),
+                          r.flops, r.bytes, ms);
+        for (const std::string& key : {r.cat, std::string("k:") + r.kern}) {
+            ProfAcc& a = c.prof[key];
+            a.calls += 1;
+            a.ms += ms;
+            a.flops += r.flops;
+            a.bytes += r.bytes;
+        }
+    }
+    if (dump) fclose(dump);
+    if (e != hipSuccess) return hip_fail(c, e, "profile");
+    return SDU_OK;
+}
+
+}  // namespace sdu

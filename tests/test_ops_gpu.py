@@ -1,0 +1,289 @@
+"""Per-op parity of the HIP kernels (through the C ABI) against the CPU oracle.
+
+Inputs are fp16-representable; the oracle computes in fp32 on the same values.
+Tolerances: fp16 storage of the output bounds the per-element error near 2^-11
+relative, so relErr_L1 <= 1e-3 for GEMM / conv / norm kernels and <= 2e-3 for
+attention (P is rounded to fp16 before the PV product), with max-abs guards.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import rel_err_l1, say
+from oracle import lcm, unet_ref as U
+
+pytestmark = pytest.mark.gpu
+
+
+def r16(shape, seed, scale=1.0, mean=0.0):
+    rng = np.random.default_rng(seed)
+    return (rng.standard_normal(shape) * scale + mean).astype(np.float16).astype(np.float32)
+
+
+def t(a):
+    return torch.from_numpy(np.ascontiguousarray(a))
+
+
+# ------------------------------------------------------------------ GroupNorm
+
+
+@pytest.mark.parametrize("B,H,W,C1,C2,silu", [
+    (2, 64, 64, 320, 0, True),      # resnet norm at level 0 (C2 batch-CFG)
+    (2, 64, 64, 320, 0, False),     # transformer input norm
+    (2, 16, 16, 1280, 1280, True),  # up-path concat 2560 @16^2
+    (1, 8, 8, 1280, 640, True),     # concat 1920 @8^2
+    (2, 32, 32, 640, 320, True),    # concat 960 @32^2
+    (3, 7, 9, 64, 0, True),         # ragged pixel count
+    (16, 8, 8, 2560, 0, False),     # C > 2048 (two channel windows per block)
+])
+def test_groupnorm(op_engine, B, H, W, C1, C2, silu):
+    say(f"groupnorm B={B} {H}x{W} C1={C1} C2={C2} silu={silu}")
+    HW, C = H * W, C1 + C2
+    x = r16((B, HW, C), 1, 2.0, 0.7)  # non-zero mean stresses the variance estimate
+    g = r16((C,), 2, 0.3, 1.0)
+    b = r16((C,), 3, 0.3)
+    e = op_engine
+    tx1 = e.upload(x[:, :, :C1].astype(np.float16))
+    tx2 = e.upload(x[:, :, C1:].astype(np.float16)) if C2 else None
+    tg, tb = e.upload(g.astype(np.float16)), e.upload(b.astype(np.float16))
+    ty = e.tensor((B, HW, C))
+    e.groupnorm(tx1, tg, tb, ty, B, HW, C1, C2, x2=tx2, silu=silu)
+    got = ty.numpy().astype(np.float32)
+    xn = t(x.transpose(0, 2, 1).reshape(B, C, H, W))
+    ref = U.group_norm(xn, t(g), t(b), act_silu=silu).numpy().reshape(B, C, HW).transpose(0, 2, 1)
+    assert rel_err_l1(got, ref) < 1e-3
+    assert np.abs(got - ref).max() < 2e-2
+    # second call on the same context (ticket counters must have reset)
+    e.groupnorm(tx1, tg, tb, ty, B, HW, C1, C2, x2=tx2, silu=silu)
+    assert np.array_equal(ty.numpy().astype(np.float32), got)
+
+
+# ------------------------------------------------------------------ LayerNorm
+
+
+@pytest.mark.parametrize("T,C", [(8192, 320), (2048, 640), (512, 1280), (128, 1280), (5, 40)])
+def test_layernorm(op_engine, T, C):
+    say(f"layernorm T={T} C={C}")
+    x = r16((T, C), 4, 3.0, -1.0)
+    g = r16((C,), 5, 0.3, 1.0)
+    b = r16((C,), 6, 0.3)
+    e = op_engine
+    tx, tg, tb = e.upload(x.astype(np.float16)), e.upload(g.astype(np.float16)), e.upload(b.astype(np.float16))
+    ty = e.tensor((T, C))
+    e.layernorm(tx, tg, tb, ty, T, C)
+    ref = U.layer_norm(t(x), t(g), t(b)).numpy()
+    got = ty.numpy().astype(np.float32)
+    assert rel_err_l1(got, ref) < 1e-3
+    assert np.abs(got - ref).max() < 2e-2
+
+
+# ------------------------------------------------------------------ matmul
+
+
+@pytest.mark.parametrize("M,N,K,K2,bias,res,geglu,f32", [
+    (8192, 320, 320, 0, True, True, False, False),    # to_out with residual, level 0
+    (8192, 960, 320, 0, False, False, False, False),  # fused QKV
+    (8192, 2560, 320, 0, True, False, True, False),   # FF proj + GEGLU
+    (8192, 320, 1280, 0, True, True, False, False),   # FF out
+    (154, 2560, 768, 0, False, False, False, False),  # cross K/V (B=2 x 77 tokens)
+    (128, 1280, 5120, 0, True, True, False, False),   # split-K (mid FF out)
+    (512, 1280, 2560, 1280, True, False, False, False),  # 1x1 shortcut over a concat
+    (77, 64, 64, 0, True, False, False, True),        # ragged M, N <= 64 tile, fp32 out
+    (100, 128, 128, 0, True, False, True, False),     # GEGLU with ragged M
+])
+def test_matmul(op_engine, M, N, K, K2, bias, res, geglu, f32):
+    say(f"matmul M={M} N={N} K={K} K2={K2} bias={bias} res={res} geglu={geglu} f32={f32}")
+    e = op_engine
+    a = r16((M, K), 7)
+    w = r16((N, K), 8, 0.05)
+    bb = r16((N,), 9, 0.5)
+    Nout = N // 2 if geglu else N
+    rr = r16((M, Nout), 10)
+    K1 = K - K2
+    ta = e.upload(a[:, :K1].astype(np.float16))
+    ta2 = e.upload(a[:, K1:].astype(np.float16)) if K2 else None
+    # GEGLU weights/bias are interleaved per 32 rows (hidden block, gate block)
+    if geglu:
+        perm = np.concatenate([np.concatenate([np.arange(j * 32, j * 32 + 32),
+                                               N // 2 + np.arange(j * 32, j * 32 + 32)])
+                               for j in range(N // 64)])
+        wd, bd = w[perm], bb[perm]
+    else:
+        wd, bd = w, bb
+    tw = e.upload(wd.astype(np.float16))
+    tb = e.upload(bd.astype(np.float16)) if bias else None
+    tr = e.upload(rr.astype(np.float16)) if res else None
+    ty = e.tensor((M, Nout), 2 if f32 else 1)
+    flags = (1 if geglu else 0) | (2 if f32 else 0)
+    e.matmul(ta, tw, ty, M, N, K, bias=tb, residual=tr, a2=ta2, K2=K2, flags=flags)
+    ref = U.linear(t(a), t(w), t(bb) if bias else None)
+    if geglu:
+        ref = U.geglu(ref)
+    if res:
+        ref = ref + t(rr)
+    ref = ref.numpy()
+    got = ty.numpy().astype(np.float32)
+    assert rel_err_l1(got, ref) < 1e-3
+    assert np.abs(got - ref).max() < 3e-2 * max(1.0, np.abs(ref).max() / 8)
+
+
+# ------------------------------------------------------------------ conv2d
+
+
+@pytest.mark.parametrize("B,H,W,Ci,Co,k,stride,ups,temb,res", [
+    (2, 64, 64, 320, 320, 3, 1, False, True, False),   # resnet conv1 @64^2 (+ time proj)
+    (2, 64, 64, 320, 320, 3, 1, False, False, True),   # resnet conv2 (+ residual)
+    (2, 64, 64, 320, 320, 3, 2, False, False, False),  # downsample
+    (2, 8, 8, 1280, 1280, 3, 1, True, False, False),   # upsample (8 -> 16)
+    (2, 8, 8, 1280, 1280, 3, 1, False, True, True),    # mid conv, split-K
+    (2, 8, 8, 2560, 1280, 3, 1, False, False, False),  # K = 23040
+    (2, 64, 64, 8, 320, 3, 1, False, False, False),    # conv_in (K = 72, tail tile)
+    (2, 64, 64, 320, 4, 3, 1, False, False, False),    # conv_out (N = 4)
+    (1, 5, 7, 16, 24, 3, 1, False, False, False),      # ragged
+    (1, 5, 7, 16, 24, 3, 2, False, False, False),      # ragged stride 2
+    (2, 32, 32, 640, 640, 1, 1, False, False, True),   # 1x1 proj
+])
+def test_conv2d(op_engine, B, H, W, Ci, Co, k, stride, ups, temb, res):
+    say(f"conv2d B={B} {H}x{W} {Ci}->{Co} k={k} s={stride} ups={ups} temb={temb} res={res}")
+    e = op_engine
+    x = r16((B, H, W, Ci), 11)
+    w = r16((Co, Ci, k, k), 12, 1.0 / math.sqrt(Ci * k * k))
+    bb = r16((Co,), 13, 0.5)
+    tp = np.random.default_rng(14).standard_normal(Co).astype(np.float32)
+    Ho = 2 * H if ups else (H - 1) // stride + 1
+    Wo = 2 * W if ups else (W - 1) // stride + 1
+    rr = r16((B, Ho, Wo, Co), 15)
+    tx = e.upload(x.astype(np.float16))
+    tw = e.upload(w.transpose(0, 2, 3, 1).astype(np.float16))  # [Co, kh, kw, Ci]
+    tb = e.upload(bb.astype(np.float16))
+    tt = e.upload(tp) if temb else None
+    tr = e.upload(rr.astype(np.float16)) if res else None
+    ty = e.tensor((B, Ho, Wo, Co))
+    e.conv2d(tx, tw, ty, B, H, W, Ci, Co, ksize=k, stride=stride, upsample=ups, bias=tb, temb=tt, residual=tr)
+    xn = t(x.transpose(0, 3, 1, 2))
+    if ups:
+        xn = U.upsample2x(xn)
+    ref = U.conv2d(xn, t(w), t(bb), stride=stride if not ups else 1, pad=k // 2)
+    if temb:
+        ref = ref + t(tp)[None, :, None, None]
+    ref = ref.numpy().transpose(0, 2, 3, 1)
+    if res:
+        ref = ref + rr
+    got = ty.numpy().astype(np.float32)
+    assert got.shape == ref.shape
+    assert rel_err_l1(got, ref) < 1e-3
+    assert np.abs(got - ref).max() < 3e-2
+
+
+# ------------------------------------------------------------------ attention
+
+
+@pytest.mark.parametrize("B,heads,Sq,Sk,d", [
+    (2, 8, 4096, 4096, 40),   # level-0 self-attention
+    (2, 8, 4096, 77, 40),     # level-0 cross-attention
+    (2, 8, 1024, 1024, 80),
+    (2, 8, 256, 256, 160),
+    (2, 8, 64, 64, 160),      # mid block
+    (2, 8, 256, 77, 160),
+    (1, 2, 100, 37, 40),      # ragged query / key counts
+    (1, 1, 1, 1, 8),          # single token
+    (1, 3, 130, 200, 64),
+])
+def test_attention(op_engine, B, heads, Sq, Sk, d):
+    say(f"attention B={B} heads={heads} Sq={Sq} Sk={Sk} d={d}")
+    e = op_engine
+    C = heads * d
+    q = r16((B, Sq, C), 16)
+    k = r16((B, Sk, C), 17)
+    v = r16((B, Sk, C), 18)
+    tq, tk, tv = e.upload(q.astype(np.float16)), e.upload(k.astype(np.float16)), e.upload(v.astype(np.float16))
+    to = e.tensor((B, Sq, C))
+    e.attention(tq, tk, tv, to, B, heads, Sq, Sk, d, C, C, C, C, 1.0 / math.sqrt(d))
+    got = to.numpy().astype(np.float32)
+    ref = U.attention(t(q), t(k), t(v), heads).numpy()
+    assert rel_err_l1(got, ref) < 2e-3
+    assert np.abs(got - ref).max() < 2e-2
+
+
+def test_attention_strided_rows(op_engine):
+    """Row strides larger than heads*d (heads read in place from a fused buffer)."""
+    e = op_engine
+    B, heads, S, d = 2, 8, 256, 40
+    C = heads * d
+    buf = r16((B, S, 3 * C), 19)
+    q, k, v = buf[..., :C], buf[..., C:2 * C], buf[..., 2 * C:]
+    # emulate column windows with three buffers padded to row stride 3C
+    pad = np.zeros((B, S, 3 * C), np.float32)
+    tq = e.upload(np.concatenate([q, pad[..., :2 * C]], -1).astype(np.float16))
+    tk = e.upload(np.concatenate([k, pad[..., :2 * C]], -1).astype(np.float16))
+    tv = e.upload(np.concatenate([v, pad[..., :2 * C]], -1).astype(np.float16))
+    to = e.tensor((B, S, 2 * C))
+    e.attention(tq, tk, tv, to, B, heads, S, S, d, 3 * C, 3 * C, 3 * C, 2 * C, 1 / math.sqrt(d))
+    got = to.numpy().astype(np.float32)[..., :C]
+    ref = U.attention(t(q), t(k), t(v), heads).numpy()
+    assert rel_err_l1(got, ref) < 2e-3
+
+
+# ------------------------------------------------------------------ elementwise
+
+
+def test_elementwise_ops(op_engine):
+    e = op_engine
+    n, C = 3 * 1000, 40
+    x = r16((n,), 20, 3.0)
+    y = r16((n,), 21)
+    b = r16((C,), 22)
+    tx, ty, tb = e.upload(x.astype(np.float16)), e.upload(y.astype(np.float16)), e.upload(b.astype(np.float16))
+    to = e.tensor((n,))
+    e.silu(tx, to, n)
+    np.testing.assert_allclose(to.numpy().astype(np.float32), U.silu(t(x)).numpy(), rtol=2e-3, atol=2e-3)
+    e.add(tx, ty, to, n)
+    np.testing.assert_allclose(to.numpy().astype(np.float32), x + y, rtol=2e-3, atol=2e-3)
+    e.add_bias(ty, tb, n, C)
+    np.testing.assert_allclose(ty.numpy().astype(np.float32), y + np.tile(b, n // C), rtol=2e-3, atol=2e-3)
+    T, C2 = 50, 64
+    g = r16((T, 2 * C2), 23, 2.0)
+    tg = e.upload(g.astype(np.float16))
+    tgo = e.tensor((T, C2))
+    e.geglu(tg, tgo, T, C2)
+    np.testing.assert_allclose(tgo.numpy().astype(np.float32), U.geglu(t(g)).numpy(), rtol=2e-3, atol=2e-3)
+
+
+@pytest.mark.parametrize("steps", [4, 1, 8])
+def test_lcm_step(op_engine, steps):
+    """CFG combine + LcmScheduler.step on the device vs the float64 oracle."""
+    e = op_engine
+    n = 4 * 32 * 32
+    rng = np.random.default_rng(24)
+    sched = lcm.LcmSchedule(steps)
+    x = rng.standard_normal(n).astype(np.float32)
+    tx = e.upload(x)
+    for idx in range(steps):
+        eps2 = rng.standard_normal((2, n)).astype(np.float32)
+        noise = rng.standard_normal(n).astype(np.float32)
+        last = idx == steps - 1
+        e.lcm_step(tx, e.upload(eps2), None if last else e.upload(noise), n, steps, idx, 8.0)
+        eps = lcm.cfg_combine(eps2[0], eps2[1], 8.0)
+        x = sched.step(idx, x, eps, None if last else noise)
+        np.testing.assert_allclose(tx.numpy(), x, rtol=1e-6, atol=1e-6)
+
+
+def test_op_argument_errors(op_engine):
+    """Bad shapes come back as status codes, not faults (vk_engine.cpp has none)."""
+    import sdu
+    e = op_engine
+    a = e.tensor((16, 16))
+    with pytest.raises(sdu.SduError) as ex:
+        e.matmul(a, a, a, 16, 16, 17)  # K not a multiple of 8
+    assert ex.value.code == sdu.SDU_ERR_ARG
+    with pytest.raises(sdu.SduError):
+        e.matmul(a, a, a, 64, 64, 64)  # tensors too small
+    with pytest.raises(sdu.SduError):
+        e.attention(a, a, a, a, 1, 1, 4, 4, 168, 168, 168, 168, 168, 1.0)  # d > 160
+    with pytest.raises(sdu.SduError):
+        e.groupnorm(a, a, a, a, 1, 16, 12, 0)  # C not a multiple of 8
+    with pytest.raises(sdu.SduError):
+        e.forward(np.zeros((1, 4, 64, 64), np.float32), np.zeros(320, np.float32),
+                  np.zeros((1, 77, 768), np.float32))  # context has no UNet weights
