@@ -20,7 +20,6 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 static constexpr int KT = 64;        // keys per iteration
-static constexpr int NWAVE = 4;      // waves per block (32 queries each)
 static constexpr int VSTR = KT + 8;  // Vt row stride (halves)
 
 __device__ __forceinline__ int key_perm(int r) {
@@ -29,8 +28,9 @@ __device__ __forceinline__ int key_perm(int r) {
     return (r & ~15) | po;
 }
 
-// KS: 16-wide k-steps covering d for QK^T; MTD: 32-row dim tiles for PV.
-template <int KS, int MTD>
+// KS: 16-wide k-steps covering d for QK^T; MTD: 32-row dim tiles for PV;
+// NWAVE: waves per block (32 queries each; they share the K/V tiles in LDS).
+template <int KS, int MTD, int NWAVE>
 __global__ __launch_bounds__(NWAVE * 64) void attn_kernel(AttnArgs a) {
     constexpr int KSTR = KS * 16 + 8;  // K row stride (halves)
     constexpr int NTH = NWAVE * 64;
@@ -190,18 +190,32 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_kernel(AttnArgs a) {
     }
 }
 
+// MINNW: the smallest block a head size may use (one-wave blocks at d > 96 would
+// need more registers for the K/V prefetch than a wave has).
+template <int KS, int MTD, int MINNW>
+static void launch_nw(const AttnArgs& a, int nw, hipStream_t s) {
+    const dim3 grid4((a.Sq + 127) / 128, a.heads, a.B), grid2((a.Sq + 63) / 64, a.heads, a.B),
+        grid1((a.Sq + 31) / 32, a.heads, a.B);
+    if (nw == 4) hipLaunchKernelGGL((attn_kernel<KS, MTD, 4>), grid4, dim3(256), 0, s, a);
+    else if (nw == 2 || MINNW > 1) hipLaunchKernelGGL((attn_kernel<KS, MTD, 2>), grid2, dim3(128), 0, s, a);
+    else hipLaunchKernelGGL((attn_kernel<KS, MTD, MINNW>), grid1, dim3(64 * MINNW), 0, s, a);
+}
+
 hipError_t attention_launch(const AttnArgs& a, hipStream_t s) {
     if (a.d <= 0 || a.d > 160 || (a.d & 7) || a.Sq <= 0 || a.Sk <= 0) return hipErrorInvalidValue;
-    dim3 grid((a.Sq + NWAVE * 32 - 1) / (NWAVE * 32), a.heads, a.B);
-    dim3 block(NWAVE * 64);
+    // fewer waves per block when the query count alone would not fill the chip
+    const int64_t bh = (int64_t)a.heads * a.B;
+    int nw = 4;
+    if (((a.Sq + 127) / 128) * bh < 512) nw = 2;
+    if (nw == 2 && ((a.Sq + 63) / 64) * bh < 512) nw = 1;
     const int d = a.d;
-    if (d <= 32) hipLaunchKernelGGL((attn_kernel<2, 1>), grid, block, 0, s, a);
-    else if (d <= 48) hipLaunchKernelGGL((attn_kernel<3, 2>), grid, block, 0, s, a);
-    else if (d <= 64) hipLaunchKernelGGL((attn_kernel<4, 2>), grid, block, 0, s, a);
-    else if (d <= 80) hipLaunchKernelGGL((attn_kernel<5, 3>), grid, block, 0, s, a);
-    else if (d <= 96) hipLaunchKernelGGL((attn_kernel<6, 3>), grid, block, 0, s, a);
-    else if (d <= 128) hipLaunchKernelGGL((attn_kernel<8, 4>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((attn_kernel<10, 5>), grid, block, 0, s, a);
+    if (d <= 32) launch_nw<2, 1, 1>(a, nw, s);
+    else if (d <= 48) launch_nw<3, 2, 1>(a, nw, s);
+    else if (d <= 64) launch_nw<4, 2, 1>(a, nw, s);
+    else if (d <= 80) launch_nw<5, 3, 1>(a, nw, s);
+    else if (d <= 96) launch_nw<6, 3, 1>(a, nw, s);
+    else if (d <= 128) launch_nw<8, 4, 2>(a, nw, s);
+    else launch_nw<10, 5, 2>(a, nw, s);
     return hipGetLastError();
 }
 

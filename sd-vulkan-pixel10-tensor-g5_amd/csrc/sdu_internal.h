@@ -51,6 +51,7 @@ struct GemmArgs {
 // Picks the tile shape and split-K factor; returns the fp32 workspace bytes the
 // launch needs (0 if none).  `ws` may be null when the return value is 0.
 size_t gemm_workspace_bytes(const GemmArgs& a);
+const char* gemm_kernel_name(const GemmArgs& a);  // tile variant the launch will use
 hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s);
 
 // y[n] = act_out( sum_k act_in(x[k]) * W[n,k] + bias[n] ), fp32 in/out, W fp16 [N,K].

@@ -62,10 +62,6 @@ struct Exec {
     }
 };
 
-static const char* gemm_kernel_name(const GemmArgs& a) {
-    return a.N <= 64 && !a.geglu ? "gemm_128x64" : "gemm_128x128";
-}
-
 static void gemm(Exec& E, const char* cat, const GemmArgs& a, double flops) {
     const size_t ws = gemm_workspace_bytes(a);
     if (ws > E.gemm_ws_need) E.gemm_ws_need = ws;
