@@ -21,8 +21,6 @@ namespace sdu {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-static constexpr int BK = 64;  // K tile (halves)
-
 __device__ __forceinline__ float gelu_erf(float x) {
     return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));
 }
@@ -62,22 +60,31 @@ __device__ __forceinline__ void wait_vmcnt_lgkm0() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0x0 << 8) | ((N >> 4) << 14));
 }
 
-// Main loop: 3-stage LDS ring fed by global_load_lds_dwordx4 (direct to LDS, no
-// register staging), so two K tiles are in flight while the third is consumed;
-// one s_barrier per K tile.  LDS rows are 128 bytes (64 halves) with the 16-byte
-// chunk index XOR-swizzled by ((row >> 1) & 7): the DMA writes stay linear per
-// wave and the 32x32x16 fragment reads (32 rows x 16 B per half-wave) are free of
-// bank conflicts.
-template <int MT, int NT, int WM, int WN>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
-    constexpr int NTH = 256, NS = 3;
-    static_assert(WM * WN == 4, "four waves");
+// Main loop: NS-stage LDS ring fed by global_load_lds_dwordx4 (direct to LDS, no
+// register staging), NS-1 K tiles in flight while one is consumed, one s_barrier
+// per K tile.  LDS rows are BK halves (64 or 128 bytes) with the 16-byte chunk
+// index XOR-swizzled per row, so the DMA writes stay linear per wave and the
+// 32x32x16 fragment reads (32 rows x 16 B per half-wave) are free of bank
+// conflicts.  Fragments are double-buffered in registers: the LDS reads of
+// k-step ks+1 are in flight during the MFMAs of k-step ks.
+template <int BKT>
+__device__ __forceinline__ int lds_swizzle(int row) {
+    return BKT == 64 ? ((row >> 1) & 7) : ((row >> 2) & 3);
+}
+
+template <int MT, int NT, int WM, int WN, int BKT, int NS>
+__global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
+    constexpr int NW = WM * WN, NTH = NW * 64;
     constexpr int TMW = MT / WM, TNW = NT / WN;  // wave tile
     constexpr int FM = TMW / 32, FN = TNW / 32;   // 32x32 MFMA tiles per wave
-    constexpr int STAGE = (MT + NT) * BK;         // halves per ring stage
-    constexpr int AI = MT / 32, BI = NT / 32;     // DMA instructions per thread per K tile
+    constexpr int CPR = BKT / 8;                  // 16-byte chunks per LDS row
+    constexpr int RPI = 1024 / (BKT * 2);         // rows one wave DMA instruction fills
+    constexpr int AI = MT / RPI / NW, BI = NT / RPI / NW;  // DMA instructions per thread per tile
     constexpr int LPT = AI + BI;
-    static_assert(MT % 32 == 0 && NT % 32 == 0 && LPT < 64, "tile shape");
+    constexpr int STAGE = (MT + NT) * BKT;        // halves per ring stage
+    constexpr int KS = BKT / 16;                  // MFMA k-steps per tile
+    static_assert(AI * RPI * NW == MT && BI * RPI * NW == NT, "DMA split");
+    static_assert(NS >= 2 && (NS - 2) * LPT < 64, "ring depth");
 
     __shared__ __attribute__((aligned(1024))) f16 smem[NS * STAGE];
 
@@ -99,17 +106,17 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
 
     const int kbeg = blockIdx.z * a.k_per_split;
     const int kend = min(a.K, kbeg + a.k_per_split);
-    const int nk = (kend - kbeg + BK - 1) / BK;
+    const int nk = (kend - kbeg + BKT - 1) / BKT;
 
     // DMA lane assignment: instruction i of wave w fills tile rows
-    // [i*32 + w*8, +8); lane l lands in row +(l>>3), physical chunk l&7, which holds
-    // logical chunk (l&7) ^ ((row>>1)&7).
-    const int lrow8 = lane >> 3, pchunk = lane & 7;
+    // [(i*NW + w)*RPI, +RPI); lane l lands in row +(l / CPR), physical chunk l % CPR,
+    // which holds logical chunk (l % CPR) ^ swizzle(row).
+    const int lr = lane / CPR, pchunk = lane % CPR;
     int a_m[AI], a_c[AI], a_b[AI], a_oy[AI], a_ox[AI];
 #pragma unroll
     for (int i = 0; i < AI; ++i) {
-        const int row = i * 32 + wave * 8 + lrow8;
-        a_c[i] = pchunk ^ ((row >> 1) & 7);
+        const int row = (i * NW + wave) * RPI + lr;
+        a_c[i] = pchunk ^ lds_swizzle<BKT>(row);
         const int m = min(m0 + row, a.M - 1);  // rows past M compute garbage that is never stored
         a_m[i] = m;
         if (a.amode == A_CONV3) {
@@ -125,20 +132,20 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
     int b_n[BI], b_c[BI];
 #pragma unroll
     for (int i = 0; i < BI; ++i) {
-        const int row = i * 32 + wave * 8 + lrow8;
-        b_c[i] = pchunk ^ ((row >> 1) & 7);
+        const int row = (i * NW + wave) * RPI + lr;
+        b_c[i] = pchunk ^ lds_swizzle<BKT>(row);
         b_n[i] = min(n0 + row, a.N - 1);
     }
-    const bool tap_uniform = (a.amode == A_CONV3) && (a.Cin % BK == 0);
+    const bool tap_uniform = (a.amode == A_CONV3) && (a.Cin % BKT == 0);
     const void* zero = (const void*)g_zero_page;
 
     // Source address of each lane's 16-byte chunk, chosen with selects (no
     // divergent branches around the DMA: exactly AI + BI DMA instructions per
     // thread and K tile, which the vmcnt waits below count on).
     auto issue = [&](int kt, int stage) __attribute__((always_inline)) {
-        const int k0 = kbeg + kt * BK;
+        const int k0 = kbeg + kt * BKT;
         f16* sA = smem + stage * STAGE;
-        f16* sB = sA + MT * BK;
+        f16* sB = sA + MT * BKT;
         if (a.amode == A_DENSE) {
 #pragma unroll
             for (int i = 0; i < AI; ++i) {
@@ -147,7 +154,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
                 const f16* base = second ? a.A2 : a.A;
                 const int64_t off = second ? (int64_t)a_m[i] * a.lda2 + (k - a.K1) : (int64_t)a_m[i] * a.lda + k;
                 const void* src = (k < kend) ? (const void*)(base + off) : zero;
-                __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(sA + (i * 32 + wave * 8) * BK),
+                __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(sA + (i * NW + wave) * RPI * BKT),
                                                  16, 0, 0);
             }
         } else {
@@ -165,7 +172,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
                 const int iy = a.upsample ? (uy >> 1) : uy, ix = a.upsample ? (ux >> 1) : ux;
                 const int64_t off = (((int64_t)a_b[i] * a.Hin + iy) * a.Win + ix) * a.Cin + c;
                 const void* src = ok ? (const void*)(a.A + off) : zero;
-                __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(sA + (i * 32 + wave * 8) * BK),
+                __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(sA + (i * NW + wave) * RPI * BKT),
                                                  16, 0, 0);
             }
         }
@@ -173,7 +180,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
         for (int i = 0; i < BI; ++i) {
             const int k = k0 + b_c[i] * 8;
             const void* src = (k < kend) ? (const void*)(a.Wt + (int64_t)b_n[i] * a.K + k) : zero;
-            __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(sB + (i * 32 + wave * 8) * BK),
+            __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(sB + (i * NW + wave) * RPI * BKT),
                                              16, 0, 0);
         }
     };
@@ -184,32 +191,35 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = floatx16{};
 
-    // fragment addressing: row (base + lrow), logical chunk 2*ks + (lane>>5)
-    const int lrow = lane & 31, hl = lane >> 5, sw = (lrow >> 1) & 7;
-    if (nk > 0) issue(0, 0);
-    if (nk > 1) issue(1, 1);
+    // fragment addressing: row (base + lrow), logical chunk 2*ks + (lane>>5);
+    // every fragment base row is a multiple of 32, so the swizzle depends on lrow only
+    const int lrow = lane & 31, hl = lane >> 5, sw = lds_swizzle<BKT>(lrow);
+#pragma unroll
+    for (int p = 0; p < NS - 1; ++p)
+        if (p < nk) issue(p, p);
     for (int kt = 0; kt < nk; ++kt) {
-        if (kt + 1 < nk) wait_vmcnt_lgkm0<LPT>();
+        // tile kt must have landed; the tiles issued after it may still be in flight
+        const int ahead = min(NS - 2, nk - 1 - kt);
+        if (ahead >= 2) wait_vmcnt_lgkm0<(NS >= 4 ? 2 * LPT : 0)>();
+        else if (ahead == 1) wait_vmcnt_lgkm0<LPT>();
         else wait_vmcnt_lgkm0<0>();
         __builtin_amdgcn_s_barrier();
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        if (kt + 2 < nk) issue(kt + 2, (kt + 2) % NS);
+        if (kt + NS - 1 < nk) issue(kt + NS - 1, (kt + NS - 1) % NS);
         const f16* sA = smem + (kt % NS) * STAGE;
-        const f16* sB = sA + MT * BK;
-        // fragments double-buffered in registers: reads of k-step ks+1 are in
-        // flight while the MFMAs of k-step ks run
+        const f16* sB = sA + MT * BKT;
         half8 af[2][FM], bf[2][FN];
         auto load_frags = [&](int ks, int slot) __attribute__((always_inline)) {
             const int pc = ((ks * 2 + hl) ^ sw) * 8;
 #pragma unroll
-            for (int i = 0; i < FM; ++i) af[slot][i] = *(const half8*)(sA + (wm * TMW + i * 32 + lrow) * BK + pc);
+            for (int i = 0; i < FM; ++i) af[slot][i] = *(const half8*)(sA + (wm * TMW + i * 32 + lrow) * BKT + pc);
 #pragma unroll
-            for (int j = 0; j < FN; ++j) bf[slot][j] = *(const half8*)(sB + (wn * TNW + j * 32 + lrow) * BK + pc);
+            for (int j = 0; j < FN; ++j) bf[slot][j] = *(const half8*)(sB + (wn * TNW + j * 32 + lrow) * BKT + pc);
         };
         load_frags(0, 0);
 #pragma unroll
-        for (int ks = 0; ks < BK / 16; ++ks) {
-            if (ks + 1 < BK / 16) load_frags(ks + 1, (ks + 1) & 1);
+        for (int ks = 0; ks < KS; ++ks) {
+            if (ks + 1 < KS) load_frags(ks + 1, (ks + 1) & 1);
 #pragma unroll
             for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -217,15 +227,17 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[ks & 1][i], bf[ks & 1][j], acc[i][j], 0, 0, 0);
         }
         // Schedule of the unrolled K tile: reads(0), reads(1), mfma(0), reads(2),
-        // mfma(1), reads(3), mfma(2), mfma(3) -- the fragments of k-step ks+1 are
-        // in flight (in their own registers) during the MFMAs of k-step ks.
-        __builtin_amdgcn_sched_group_barrier(0x100, 2 * (FM + FN), 0);  // DS reads
+        // mfma(1), ... -- the fragments of k-step ks+1 are in flight during the
+        // MFMAs of k-step ks.
+        if (KS >= 2) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 2 * (FM + FN), 0);  // DS reads
 #pragma unroll
-        for (int ks = 0; ks < BK / 16 - 2; ++ks) {
-            __builtin_amdgcn_sched_group_barrier(0x008, FM * FN, 0);  // MFMAs
-            __builtin_amdgcn_sched_group_barrier(0x100, FM + FN, 0);  // DS reads
+            for (int ks = 0; ks < KS - 2; ++ks) {
+                __builtin_amdgcn_sched_group_barrier(0x008, FM * FN, 0);  // MFMAs
+                __builtin_amdgcn_sched_group_barrier(0x100, FM + FN, 0);  // DS reads
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 2 * FM * FN, 0);
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, 2 * FM * FN, 0);
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
     }
 
@@ -247,106 +259,110 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
             }
         return;
     }
-    // Stage the fp32 tile through LDS (reusing the operand ring).  The vector path
-    // then gives each thread one fixed 8-column slice of several rows: epilogue
-    // operands are all loaded before any store (the residual may alias the
-    // output), and stores are 16-byte.
+    // The fp32 tile goes through LDS (reusing the ring) in FM passes of WM*32 rows
+    // (rows wm*TMW + i*32 + [0,32) of pass i).  In the vector path each thread owns
+    // one fixed 8-column slice: bias / residual of a pass are all loaded before any
+    // store (the residual may alias the output), and stores are 16-byte.
+    constexpr int PR = WM * 32;  // staged rows per pass
     constexpr int CST = NT + 4;  // padded fp32 row stride
-    static_assert(MT * CST * 4 <= NS * STAGE * 2, "C tile fits the operand LDS");
+    static_assert(PR * CST * 4 <= NS * STAGE * 2, "C pass fits the operand LDS");
     float* Cs = (float*)smem;
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int r = wm * TMW + i * 32 + (e >> 2) * 8 + rq + (e & 3);
-                Cs[r * CST + wn * TNW + j * 32 + col_l] = acc[i][j][e];
-            }
-    __syncthreads();
-    if (a.out_mode == OUT_F32_NCHW || (a.N & 7)) {
-        // narrow outputs (conv_out, N = 4): one element per thread iteration
-        const int nto = a.geglu ? NT / 2 : NT;
-        for (int idx = tid; idx < MT * nto; idx += NTH) {
-            const int r = idx / nto, oc = idx - r * nto;
-            const int tc = a.geglu ? (oc >> 5) * 64 + (oc & 31) : oc;
-            const int m = m0 + r, n = n0 + tc;
-            if (m >= a.M || n >= a.N) continue;
-            const int nout = a.geglu ? (n0 >> 1) + oc : n;
-            epi_store(a, m, n, Cs[r * CST + tc], a.geglu ? Cs[r * CST + tc + 32] : 0.f, nout);
-        }
-        return;
-    }
+    const bool narrow = a.out_mode == OUT_F32_NCHW || (a.N & 7);
     const int NTO = NT / (a.geglu ? 2 : 1);  // output columns of this tile
     const int cpr = NTO / 8;                  // 8-column chunks per row
     const int oc = (tid % cpr) * 8;           // fixed output column slice of this thread
     const int r0 = tid / cpr, rstep = NTH / cpr;
-    // tile column of the (first) source value for output column oc
-    const int tc = a.geglu ? (oc >> 5) * 64 + (oc & 31) : oc;
+    const int tc = a.geglu ? (oc >> 5) * 64 + (oc & 31) : oc;  // tile column of oc's source
     const int n = n0 + tc;
     const int nout = a.geglu ? (n0 >> 1) + oc : n;
-    if (n >= a.N) return;
     float badd[8], gadd[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) { badd[e] = 0.f; gadd[e] = 0.f; }
-    if (a.bias) {
-        const uint4 bv = *(const uint4*)(a.bias + n);
-        const f16* bh = (const f16*)&bv;
+    if (!narrow && n < a.N) {
+        if (a.bias) {
+            const uint4 bv = *(const uint4*)(a.bias + n);
+            const f16* bh = (const f16*)&bv;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) badd[e] = (float)bh[e];
-        if (a.geglu) {
-            const uint4 gv = *(const uint4*)(a.bias + n + 32);
-            const f16* gh = (const f16*)&gv;
+            for (int e = 0; e < 8; ++e) badd[e] = (float)bh[e];
+            if (a.geglu) {
+                const uint4 gv = *(const uint4*)(a.bias + n + 32);
+                const f16* gh = (const f16*)&gv;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) gadd[e] = (float)gh[e];
+                for (int e = 0; e < 8; ++e) gadd[e] = (float)gh[e];
+            }
+        }
+        if (a.bias2) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) badd[e] += a.bias2[n + e];
+            if (a.geglu) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) gadd[e] += a.bias2[n + 32 + e];
+            }
         }
     }
-    if (a.bias2) {
+    constexpr int MAXR = PR * (NT / 8) / NTH;  // staged rows per thread per pass (non-GEGLU)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) badd[e] += a.bias2[n + e];
-        if (a.geglu) {
+    for (int ip = 0; ip < FM; ++ip) {
+        __syncthreads();
 #pragma unroll
-            for (int e = 0; e < 8; ++e) gadd[e] += a.bias2[n + 32 + e];
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int r = wm * 32 + (e >> 2) * 8 + rq + (e & 3);
+                Cs[r * CST + wn * TNW + j * 32 + col_l] = acc[ip][j][e];
+            }
+        __syncthreads();
+        // staged row s <-> tile row (s / 32) * TMW + ip * 32 + s % 32
+        if (narrow) {
+            const int nto = a.geglu ? NT / 2 : NT;
+            for (int idx = tid; idx < PR * nto; idx += NTH) {
+                const int sr = idx / nto, o = idx - sr * nto;
+                const int t = a.geglu ? (o >> 5) * 64 + (o & 31) : o;
+                const int m = m0 + (sr >> 5) * TMW + ip * 32 + (sr & 31), nn = n0 + t;
+                if (m >= a.M || nn >= a.N) continue;
+                epi_store(a, m, nn, Cs[sr * CST + t], a.geglu ? Cs[sr * CST + t + 32] : 0.f,
+                          a.geglu ? (n0 >> 1) + o : nn);
+            }
+            continue;
         }
-    }
-    constexpr int MAXR = MT * NT / 8 / NTH;  // rows per thread (non-GEGLU; GEGLU uses half)
-    uint4 rres[MAXR];
-    if (a.res) {
+        if (n >= a.N) continue;
+        uint4 rres[MAXR];
+        if (a.res) {
+#pragma unroll
+            for (int k = 0; k < MAXR; ++k) {
+                const int sr = r0 + k * rstep;
+                const int m = m0 + (sr >> 5) * TMW + ip * 32 + (sr & 31);
+                rres[k] = make_uint4(0, 0, 0, 0);
+                if (sr < PR && m < a.M) rres[k] = *(const uint4*)(a.res + (int64_t)m * a.ldr + nout);
+            }
+        }
 #pragma unroll
         for (int k = 0; k < MAXR; ++k) {
-            const int r = r0 + k * rstep;
-            const int m = m0 + r;
-            rres[k] = make_uint4(0, 0, 0, 0);
-            if (r < MT && m < a.M) rres[k] = *(const uint4*)(a.res + (int64_t)m * a.ldr + nout);
-        }
-    }
+            const int sr = r0 + k * rstep;
+            const int m = m0 + (sr >> 5) * TMW + ip * 32 + (sr & 31);
+            if (sr >= PR || m >= a.M) continue;
+            float v[8];
 #pragma unroll
-    for (int k = 0; k < MAXR; ++k) {
-        const int r = r0 + k * rstep;
-        const int m = m0 + r;
-        if (r >= MT || m >= a.M) continue;
-        float v[8];
+            for (int e = 0; e < 8; ++e) {
+                v[e] = Cs[sr * CST + tc + e] + badd[e];
+                if (a.geglu) v[e] *= gelu_erf(Cs[sr * CST + tc + 32 + e] + gadd[e]);
+            }
+            if (a.res) {
+                const f16* rh = (const f16*)&rres[k];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            v[e] = Cs[r * CST + tc + e] + badd[e];
-            if (a.geglu) v[e] *= gelu_erf(Cs[r * CST + tc + 32 + e] + gadd[e]);
-        }
-        if (a.res) {
-            const f16* rh = (const f16*)&rres[k];
+                for (int e = 0; e < 8; ++e) v[e] += (float)rh[e];
+            }
+            if (a.out_mode == OUT_F16) {
+                uint4 o;
+                f16* oh = (f16*)&o;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) v[e] += (float)rh[e];
-        }
-        if (a.out_mode == OUT_F16) {
-            uint4 o;
-            f16* oh = (f16*)&o;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) oh[e] = (f16)v[e];
-            *(uint4*)((f16*)a.C + (int64_t)m * a.ldc + nout) = o;
-        } else {
-            float* cp = (float*)a.C + (int64_t)m * a.ldc + nout;
-            *(float4*)cp = make_float4(v[0], v[1], v[2], v[3]);
-            *(float4*)(cp + 4) = make_float4(v[4], v[5], v[6], v[7]);
+                for (int e = 0; e < 8; ++e) oh[e] = (f16)v[e];
+                *(uint4*)((f16*)a.C + (int64_t)m * a.ldc + nout) = o;
+            } else {
+                float* cp = (float*)a.C + (int64_t)m * a.ldc + nout;
+                *(float4*)cp = make_float4(v[0], v[1], v[2], v[3]);
+                *(float4*)(cp + 4) = make_float4(v[4], v[5], v[6], v[7]);
+            }
         }
     }
 }
@@ -424,24 +440,33 @@ struct Cfg {
     double eff;          // relative per-FLOP throughput of the tile shape
     const char* name;
 };
-// 256x128: waves 128x64; 128x128: waves 64x64; 128x64: waves 64x32.
-const Cfg kCfgs[3] = {{256, 128, 1, 1.0, "gemm_256x128"},
-                      {128, 128, 1, 0.8, "gemm_128x128"},
-                      {128, 64, 2, 0.6, "gemm_128x64"}};
+// 0: 256x128, 8 waves of 64x64, BK 64, 2-stage ring (96 KB LDS, one block per CU)
+// 1: 128x128, 4 waves of 64x64, BK 32, 4-stage ring (64 KB, two per CU)
+// 2: 128x64,  4 waves of 64x32, BK 32, 4-stage ring (48 KB, three per CU)
+// 3: 128x128, 4 waves of 64x64, BK 64, 2-stage ring (64 KB, two per CU)
+const Cfg kCfgs[4] = {{256, 128, 1, 1.0, "gemm_256x128"},
+                      {128, 128, 2, 0.95, "gemm_128x128"},
+                      {128, 64, 3, 0.75, "gemm_128x64"},
+                      {128, 128, 2, 0.95, "gemm_128x128k64"}};
 
 int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
-// Pick the tile shape and split-K factor with the lowest modelled time:
-// block waves over 256 CUs x per-block MFMA time, plus the fp32 partial round
-// trip and the reduce launch when K is split.
+// Pick the tile shape and split-K factor with the lowest modelled time.  A block
+// that has its CU to itself runs at the full per-CU rate; blocks sharing a CU
+// split it.  Each block also pays a fixed prologue / epilogue cost, and a split
+// K pays the fp32 partial round trip plus the reduce launch.
 void plan(const GemmArgs& a, int& ci, int& splits, int& kps) {
-    const double cu_flops = 2.5e15 / 256.0;
-    const int nkt = ceil_div(a.K, BK);
+    const double cu_rate = 2.5e12;  // sustained MFMA FLOP/s per CU for these tiles
+    const double t_block = 2.0e-6;  // per-block fixed cost
+    const int nkt = ceil_div(a.K, 64);
     double best = 1e30;
-    ci = 0; splits = 1; kps = nkt * BK;
-    for (int c = 0; c < 3; ++c) {
+    ci = 1; splits = 1; kps = nkt * 64;
+    for (int c = 0; c < 4; ++c) {
         const Cfg& g = kCfgs[c];
         if (a.geglu && g.nt < 128) continue;  // GEGLU pairs 32-column blocks within a 64-wide wave tile
+        // the implicit-GEMM conv gathers are cheaper per FLOP with 64-wide K tiles
+        if (a.amode == A_CONV3 && c == 1) continue;
+        if (a.amode != A_CONV3 && c == 3) continue;
         const int tiles = ceil_div(a.M, g.mt) * ceil_div(a.N, g.nt);
         static const int cand[] = {1, 2, 3, 4, 6, 8, 12, 16, 24, 32};
         for (int s : cand) {
@@ -449,12 +474,12 @@ void plan(const GemmArgs& a, int& ci, int& splits, int& kps) {
             const int kt_per = ceil_div(nkt, s);
             const int se = ceil_div(nkt, kt_per);
             const long blocks = (long)tiles * se;
-            const long slots = 256L * g.per_cu;
-            const long waves = (blocks + slots - 1) / slots;
-            const double blk_t = 2.0 * g.mt * g.nt * kt_per * BK * g.per_cu / (g.eff * cu_flops);
-            double t = waves * blk_t + 1.5e-6;
+            const int conc = (int)std::min<long>(g.per_cu, (blocks + 255) / 256);
+            const long rounds = (blocks + 256L * conc - 1) / (256L * conc);
+            const double work = 2.0 * g.mt * g.nt * kt_per * 64.0;
+            double t = rounds * (work * conc / (g.eff * cu_rate) + t_block);
             if (se > 1) t += (double)se * a.M * a.N * 8.0 / 4.0e12 + 2.5e-6;
-            if (t < best * 0.97) { best = t; ci = c; splits = se; kps = kt_per * BK; }
+            if (t < best * 0.98) { best = t; ci = c; splits = se; kps = kt_per * 64; }
         }
     }
 }
@@ -482,9 +507,10 @@ hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s) {
     if (splits > 1 && ws == nullptr) return hipErrorInvalidValue;
     const Cfg& g = kCfgs[ci];
     dim3 grid(ceil_div(a.M, g.mt) * ceil_div(a.N, g.nt), 1, splits);
-    if (ci == 0) hipLaunchKernelGGL((gemm_kernel<256, 128, 2, 2>), grid, dim3(256), 0, s, a);
-    else if (ci == 1) hipLaunchKernelGGL((gemm_kernel<128, 128, 2, 2>), grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((gemm_kernel<128, 64, 2, 2>), grid, dim3(256), 0, s, a);
+    if (ci == 0) hipLaunchKernelGGL((gemm_kernel<256, 128, 4, 2, 64, 2>), grid, dim3(512), 0, s, a);
+    else if (ci == 1) hipLaunchKernelGGL((gemm_kernel<128, 128, 2, 2, 32, 4>), grid, dim3(256), 0, s, a);
+    else if (ci == 2) hipLaunchKernelGGL((gemm_kernel<128, 64, 2, 2, 32, 4>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((gemm_kernel<128, 128, 2, 2, 64, 2>), grid, dim3(256), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || splits == 1) return e;
     const int nout = a.geglu ? a.N / 2 : a.N;
