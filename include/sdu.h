@@ -104,10 +104,14 @@ int sdu_denoise_lcm_device(sdu_ctx* ctx, const float* d_lat, const float* d_cond
  * relErr_L1 = sum|ref-got| / sum|ref| over the three outputs; negative on error. */
 double sdu_selftest(sdu_ctx* ctx, const char* fixture_dir);
 
-/* unetProfile (vk_engine.cpp:854-872): one eager forward, each kernel timed with
- * HIP events on the context stream, accumulated per category. */
+/* unetProfile (vk_engine.cpp:854-872): one eager forward in which every kernel
+ * launch is timed on its own with HIP events on the context stream (the launch is
+ * repeated SDU_PROFILE_REPS times, default 5, between its events and the average
+ * kept).  Entries are accumulated per op category (e.g. "conv3x3") and per kernel
+ * ("k:" + kernel name, e.g. "k:gemm_kernel<128,128,2,2,64,2>"); total_ms sums the
+ * categories.  The activations of the profiled pass are not meaningful. */
 typedef struct sdu_prof_entry {
-    char name[32];
+    char name[48];
     int calls;
     double ms;      /* summed kernel time */
     double flops;   /* algorithmic FLOPs over those calls */

@@ -196,9 +196,18 @@ template <int KS, int MTD, int MINNW>
 static void launch_nw(const AttnArgs& a, int nw, hipStream_t s) {
     const dim3 grid4((a.Sq + 127) / 128, a.heads, a.B), grid2((a.Sq + 63) / 64, a.heads, a.B),
         grid1((a.Sq + 31) / 32, a.heads, a.B);
-    if (nw == 4) hipLaunchKernelGGL((attn_kernel<KS, MTD, 4>), grid4, dim3(256), 0, s, a);
-    else if (nw == 2 || MINNW > 1) hipLaunchKernelGGL((attn_kernel<KS, MTD, 2>), grid2, dim3(128), 0, s, a);
-    else hipLaunchKernelGGL((attn_kernel<KS, MTD, MINNW>), grid1, dim3(64 * MINNW), 0, s, a);
+    if (nw < 2 && MINNW > 1) nw = 2;
+    char name[32];
+    snprintf(name, sizeof name, "attn_kernel<%d,%d,%d>", KS, MTD, nw);
+    // algorithmic work: QK^T and PV at the true head size; Q, K, V read and O written once
+    const double bh = (double)a.B * a.heads;
+    const double flops = 4.0 * bh * a.Sq * a.Sk * a.d;
+    const double bytes = 2.0 * bh * a.d * (2.0 * a.Sq + 2.0 * a.Sk);
+    launch_timed(name, flops, bytes, [&] {
+        if (nw == 4) hipLaunchKernelGGL((attn_kernel<KS, MTD, 4>), grid4, dim3(256), 0, s, a);
+        else if (nw == 2) hipLaunchKernelGGL((attn_kernel<KS, MTD, 2>), grid2, dim3(128), 0, s, a);
+        else hipLaunchKernelGGL((attn_kernel<KS, MTD, MINNW>), grid1, dim3(64 * MINNW), 0, s, a);
+    });
 }
 
 hipError_t attention_launch(const AttnArgs& a, hipStream_t s) {

@@ -507,16 +507,30 @@ hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s) {
     if (splits > 1 && ws == nullptr) return hipErrorInvalidValue;
     const Cfg& g = kCfgs[ci];
     dim3 grid(ceil_div(a.M, g.mt) * ceil_div(a.N, g.nt), 1, splits);
-    if (ci == 0) hipLaunchKernelGGL((gemm_kernel<256, 128, 4, 2, 64, 2>), grid, dim3(512), 0, s, a);
-    else if (ci == 1) hipLaunchKernelGGL((gemm_kernel<128, 128, 2, 2, 32, 4>), grid, dim3(256), 0, s, a);
-    else if (ci == 2) hipLaunchKernelGGL((gemm_kernel<128, 64, 2, 2, 32, 4>), grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((gemm_kernel<128, 128, 2, 2, 64, 2>), grid, dim3(256), 0, s, a);
+    // algorithmic traffic: A once (the conv source image, not its im2col), W once, output
+    // (+ residual) once; a split pays its fp32 partials out and back
+    const int nout = a.geglu ? a.N / 2 : a.N;
+    const double a_bytes = a.amode == A_CONV3 ? 2.0 * a.Bn * a.Hin * a.Win * a.Cin : 2.0 * a.M * a.K;
+    const double out_bytes = (double)a.M * nout * (a.out_mode == OUT_F16 ? 2.0 : 4.0) +
+                             (a.res ? 2.0 * a.M * nout : 0.0);
+    const double part_bytes = splits > 1 ? 4.0 * splits * a.M * a.N : 0.0;
+    const double flops = 2.0 * a.M * a.N * a.K;
+    const double k_bytes = a_bytes + 2.0 * a.N * a.K + (splits > 1 ? part_bytes : out_bytes);
+    static const char* kNames[4] = {"gemm_kernel<256,128,4,2,64,2>", "gemm_kernel<128,128,2,2,32,4>",
+                                    "gemm_kernel<128,64,2,2,32,4>", "gemm_kernel<128,128,2,2,64,2>"};
+    launch_timed(kNames[ci], flops, k_bytes, [&] {
+        if (ci == 0) hipLaunchKernelGGL((gemm_kernel<256, 128, 4, 2, 64, 2>), grid, dim3(512), 0, s, a);
+        else if (ci == 1) hipLaunchKernelGGL((gemm_kernel<128, 128, 2, 2, 32, 4>), grid, dim3(256), 0, s, a);
+        else if (ci == 2) hipLaunchKernelGGL((gemm_kernel<128, 64, 2, 2, 32, 4>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((gemm_kernel<128, 128, 2, 2, 64, 2>), grid, dim3(256), 0, s, a);
+    });
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || splits == 1) return e;
-    const int nout = a.geglu ? a.N / 2 : a.N;
     const bool vec = a.out_mode != OUT_F32_NCHW && (a.N & 7) == 0;
     const int64_t total = (int64_t)a.M * (vec ? nout / 8 : nout);
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, a);
+    launch_timed("splitk_reduce_kernel", 0.0, part_bytes + out_bytes, [&] {
+        hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, a);
+    });
     return hipGetLastError();
 }
 
@@ -552,8 +566,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* x, const f16* W,
 
 hipError_t gemv_launch(const float* x, const f16* W, const f16* bias, float* y, int N, int K,
                        int act_in, int act_out, hipStream_t s) {
-    hipLaunchKernelGGL(gemv_kernel, dim3((N + 3) / 4), dim3(256), 0, s, x, W, bias, y, N, K, act_in,
-                       act_out);
+    launch_timed("gemv_kernel", 2.0 * N * K, 2.0 * N * K + 4.0 * (N + K), [&] {
+        hipLaunchKernelGGL(gemv_kernel, dim3((N + 3) / 4), dim3(256), 0, s, x, W, bias, y, N, K, act_in,
+                           act_out);
+    });
     return hipGetLastError();
 }
 

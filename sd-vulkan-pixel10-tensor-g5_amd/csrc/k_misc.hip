@@ -30,8 +30,10 @@ __global__ void nchw_to_nhwc_kernel(const float* src, f16* dst, int B, int Bsrc,
 hipError_t nchw_to_nhwc_launch(const float* src, f16* dst, int B, int Bsrc, int C, int Cpad, int HW,
                                hipStream_t s) {
     const int64_t total = (int64_t)B * HW * Cpad;
-    hipLaunchKernelGGL(nchw_to_nhwc_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
-                       src, dst, B, Bsrc, C, Cpad, HW);
+    launch_timed("nchw_to_nhwc_kernel", 0.0, 4.0 * Bsrc * C * HW + 2.0 * total, [&] {
+        hipLaunchKernelGGL(nchw_to_nhwc_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                           src, dst, B, Bsrc, C, Cpad, HW);
+    });
     return hipGetLastError();
 }
 
@@ -44,11 +46,15 @@ __global__ void f16_to_f32_kernel(const f16* src, float* dst, int64_t n) {
     if (i < n) dst[i] = (float)src[i];
 }
 hipError_t f32_to_f16_launch(const float* src, f16* dst, int64_t n, hipStream_t s) {
-    hipLaunchKernelGGL(f32_to_f16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src, dst, n);
+    launch_timed("f32_to_f16_kernel", 0.0, 6.0 * n, [&] {
+        hipLaunchKernelGGL(f32_to_f16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src, dst, n);
+    });
     return hipGetLastError();
 }
 hipError_t f16_to_f32_launch(const f16* src, float* dst, int64_t n, hipStream_t s) {
-    hipLaunchKernelGGL(f16_to_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src, dst, n);
+    launch_timed("f16_to_f32_kernel", 0.0, 6.0 * n, [&] {
+        hipLaunchKernelGGL(f16_to_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src, dst, n);
+    });
     return hipGetLastError();
 }
 
@@ -132,8 +138,10 @@ __global__ void lcm_step_kernel(float* x, const float* eps2, const float* noise,
 
 hipError_t lcm_step_launch(float* x, const float* eps2, const float* noise, int64_t n, LcmCoeffs c,
                            f16* unet_in, int C, int HW, int Cpad, hipStream_t s) {
-    hipLaunchKernelGGL(lcm_step_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, eps2,
-                       noise, n, c, unet_in, C, HW, Cpad);
+    launch_timed("lcm_step_kernel", 0.0, 16.0 * n, [&] {
+        hipLaunchKernelGGL(lcm_step_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, eps2,
+                           noise, n, c, unet_in, C, HW, Cpad);
+    });
     return hipGetLastError();
 }
 

@@ -156,7 +156,9 @@ __global__ void zero_kernel(uint4* p, int64_t n16) {
 hipError_t zero_launch(void* p, size_t bytes, hipStream_t s) {
     const int64_t n16 = (int64_t)((bytes + 15) / 16);
     if (n16 == 0) return hipSuccess;
-    hipLaunchKernelGGL(zero_kernel, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0, s, (uint4*)p, n16);
+    launch_timed("zero_kernel", 0.0, 16.0 * n16, [&] {
+        hipLaunchKernelGGL(zero_kernel, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0, s, (uint4*)p, n16);
+    });
     return hipGetLastError();
 }
 
@@ -166,12 +168,17 @@ hipError_t groupnorm_launch(const f16* x, const f16* x2, int C1, int C2, const f
     const int C = C1 + C2;
     if (G > GN_MAXG || C > GN_MAXC || C % G || C % 8 || C1 % 8 || (C2 && !x2)) return hipErrorInvalidValue;
     GnGeom g = gn_geom(HW, C);
-    hipLaunchKernelGGL(gn_stats_kernel, dim3(g.nchunk, B), dim3(GN_THREADS), 0, s, x, x2, C1, C2, HW, g.P,
-                       G, acc);
+    const double xbytes = 2.0 * B * HW * C;
+    launch_timed("gn_stats_kernel", 0.0, xbytes, [&] {
+        hipLaunchKernelGGL(gn_stats_kernel, dim3(g.nchunk, B), dim3(GN_THREADS), 0, s, x, x2, C1, C2, HW,
+                           g.P, G, acc);
+    });
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(gn_apply_kernel, dim3(g.nchunk, B), dim3(GN_THREADS), 0, s, x, x2, C1, C2, gamma,
-                       beta, y, HW, g.P, G, eps, silu, (const double*)acc);
+    launch_timed("gn_apply_kernel", 0.0, 2.0 * xbytes, [&] {
+        hipLaunchKernelGGL(gn_apply_kernel, dim3(g.nchunk, B), dim3(GN_THREADS), 0, s, x, x2, C1, C2, gamma,
+                           beta, y, HW, g.P, G, eps, silu, (const double*)acc);
+    });
     return hipGetLastError();
 }
 
@@ -231,10 +238,14 @@ hipError_t layernorm_launch(const f16* x, const f16* gamma, const f16* beta, f16
                             float eps, hipStream_t s) {
     if (C % 8 || C > 4 * 512) return hipErrorInvalidValue;
     dim3 grid((T + 3) / 4), block(256);
-    if (C <= 512) hipLaunchKernelGGL(ln_kernel<1>, grid, block, 0, s, x, gamma, beta, y, T, C, eps);
-    else if (C <= 1024) hipLaunchKernelGGL(ln_kernel<2>, grid, block, 0, s, x, gamma, beta, y, T, C, eps);
-    else if (C <= 1536) hipLaunchKernelGGL(ln_kernel<3>, grid, block, 0, s, x, gamma, beta, y, T, C, eps);
-    else hipLaunchKernelGGL(ln_kernel<4>, grid, block, 0, s, x, gamma, beta, y, T, C, eps);
+    static const char* kNames[4] = {"ln_kernel<1>", "ln_kernel<2>", "ln_kernel<3>", "ln_kernel<4>"};
+    const int v = C <= 512 ? 0 : C <= 1024 ? 1 : C <= 1536 ? 2 : 3;
+    launch_timed(kNames[v], 0.0, 4.0 * T * C, [&] {
+        if (v == 0) hipLaunchKernelGGL(ln_kernel<1>, grid, block, 0, s, x, gamma, beta, y, T, C, eps);
+        else if (v == 1) hipLaunchKernelGGL(ln_kernel<2>, grid, block, 0, s, x, gamma, beta, y, T, C, eps);
+        else if (v == 2) hipLaunchKernelGGL(ln_kernel<3>, grid, block, 0, s, x, gamma, beta, y, T, C, eps);
+        else hipLaunchKernelGGL(ln_kernel<4>, grid, block, 0, s, x, gamma, beta, y, T, C, eps);
+    });
     return hipGetLastError();
 }
 

@@ -12,6 +12,26 @@ namespace sdu {
 
 typedef _Float16 f16;
 
+// ----------------------------------------------------------------- kernel timing
+// Eager profiling hook.  While a KernelTimer is installed on the calling thread
+// (only inside sdu_profile, never during graph capture), every kernel launch of
+// the k_*.hip launchers goes through it with its algorithmic FLOPs and HBM bytes,
+// so that each kernel is timed on its own.
+struct KernelTimer {
+    virtual ~KernelTimer() = default;
+    virtual void run(const char* kernel, double flops, double bytes, void (*fn)(const void*),
+                     const void* arg) = 0;
+};
+extern thread_local KernelTimer* g_kernel_timer;
+
+template <class F>
+inline void launch_timed(const char* kernel, double flops, double bytes, const F& f) {
+    if (g_kernel_timer)
+        g_kernel_timer->run(kernel, flops, bytes, [](const void* p) { (*(const F*)p)(); }, &f);
+    else
+        f();
+}
+
 // ----------------------------------------------------------------- GEMM
 // C[M,N] = A[M,K] . W[N,K]^T with a fused epilogue.  A is either a dense
 // row-major matrix (optionally split over two sources along K) or the implicit

@@ -7,6 +7,7 @@
 // reference records one command buffer per forward, :714, :783-788).
 #include "engine.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -21,10 +22,34 @@ static const int kLatC = 4, kLatCpad = 8, kCtxDim = 768;
 
 // ------------------------------------------------------------------ execution
 
+thread_local KernelTimer* g_kernel_timer = nullptr;
+
 struct ProfRec {
     std::string cat, kern, shape;
     double flops, bytes;
+    int reps;
     hipEvent_t e0, e1;
+};
+
+// Times every kernel launch on its own: the launch is issued `reps` times back to
+// back between two events, so the per-launch figure is the steady-state duration
+// of that kernel on a busy stream, as in a graph replay.
+struct EventTimer : KernelTimer {
+    hipStream_t s;
+    int reps = 5;
+    std::string cat, shape;
+    std::vector<ProfRec> recs;
+    void run(const char* kernel, double flops, double bytes, void (*fn)(const void*), const void* arg) override {
+        ProfRec pr;
+        pr.cat = cat; pr.kern = kernel; pr.shape = shape;
+        pr.flops = flops; pr.bytes = bytes; pr.reps = reps;
+        hipEventCreate(&pr.e0);
+        hipEventCreate(&pr.e1);
+        hipEventRecord(pr.e0, s);
+        for (int r = 0; r < reps; ++r) fn(arg);
+        hipEventRecord(pr.e1, s);
+        recs.push_back(pr);
+    }
 };
 
 struct Exec {
@@ -37,41 +62,29 @@ struct Exec {
     size_t gemm_ws_need = 0;
     double* gn_acc = nullptr;  // next free GroupNorm accumulator slot (zeroed per forward)
     hipError_t err = hipSuccess;
-    std::vector<ProfRec>* prof = nullptr;
+    EventTimer* timer = nullptr;  // eager profiling only
 
     template <class T>
     T* alloc(size_t n) { return (T*)ar->alloc(n * sizeof(T)); }
 
+    // One op: `cat` names the op category; the kernels it launches report their own
+    // names, FLOPs and bytes to the timer when profiling.
     template <class F>
-    void run(const char* cat, const char* kern, double flops, double bytes, F&& launch,
-             const std::string& shape = std::string()) {
+    void run(const char* cat, F&& launch, const std::string& shape = std::string()) {
         if (dry || err != hipSuccess) return;
-        ProfRec pr;
-        if (prof) {
-            pr.cat = cat; pr.kern = kern; pr.flops = flops; pr.bytes = bytes; pr.shape = shape;
-            hipEventCreate(&pr.e0);
-            hipEventCreate(&pr.e1);
-            hipEventRecord(pr.e0, s);
-        }
+        if (timer) { timer->cat = cat; timer->shape = shape; }
         hipError_t e = launch();
         if (e != hipSuccess) err = e;
-        if (prof) {
-            hipEventRecord(pr.e1, s);
-            prof->push_back(pr);
-        }
     }
 };
 
-static void gemm(Exec& E, const char* cat, const GemmArgs& a, double flops) {
+static void gemm(Exec& E, const char* cat, const GemmArgs& a) {
     const size_t ws = gemm_workspace_bytes(a);
     if (ws > E.gemm_ws_need) E.gemm_ws_need = ws;
-    const double out_el = (double)a.M * (a.geglu ? a.N / 2 : a.N);
-    const double bytes = 2.0 * ((double)a.M * a.K + (double)a.N * a.K) +
-                         out_el * (a.out_mode == OUT_F16 ? 2.0 : 4.0) + (a.res ? out_el * 2.0 : 0.0);
     char shape[96];
     snprintf(shape, sizeof shape, "%s M=%d N=%d K=%d geglu=%d", a.amode == A_CONV3 ? "conv3" : "dense",
              a.M, a.N, a.K, a.geglu);
-    E.run(cat, gemm_kernel_name(a), flops, bytes, [&] { return gemm_launch(a, E.gemm_ws, E.s); }, shape);
+    E.run(cat, [&] { return gemm_launch(a, E.gemm_ws, E.s); }, shape);
 }
 
 static GemmArgs dense_args(const f16* A, int lda, int M, int N, int K, const f16* W, void* C, int ldc) {
@@ -106,30 +119,24 @@ static void groupnorm(Exec& E, const f16* x, const f16* x2, int C1, int C2, cons
                       const f16* b, f16* y, int HW, int silu) {
     double* acc = E.gn_acc;
     E.gn_acc += (size_t)E.B * kGroups * 2;
-    const double bytes = 4.0 * E.B * HW * (C1 + C2);
     char shape[48];
     snprintf(shape, sizeof shape, "HW=%d C=%d", HW, C1 + C2);
-    E.run(silu ? "groupnorm_silu" : "groupnorm", "groupnorm", 0, bytes, [&] {
+    E.run(silu ? "groupnorm_silu" : "groupnorm", [&] {
         return groupnorm_launch(x, x2, C1, C2, g, b, y, E.B, HW, kGroups, kEps, silu, acc, E.s);
     }, shape);
 }
 
 static void layernorm(Exec& E, const f16* x, const f16* g, const f16* b, f16* y, int T, int C) {
-    E.run("layernorm", "layernorm", 0, 4.0 * T * C,
-          [&] { return layernorm_launch(x, g, b, y, T, C, kEps, E.s); });
+    E.run("layernorm", [&] { return layernorm_launch(x, g, b, y, T, C, kEps, E.s); });
 }
 
 static void attention(Exec& E, const char* cat, const f16* q, const f16* k, const f16* v, f16* o,
                       int Sq, int Sk, int C, int ldq, int ldk, int ldv) {
     AttnArgs a{q, k, v, o, E.B, kHeads, Sq, Sk, C / kHeads, ldq, ldk, ldv, C,
                1.0f / sqrtf((float)(C / kHeads))};
-    const double flops = 4.0 * E.B * kHeads * (double)Sq * Sk * (C / kHeads);
-    const double bytes = 2.0 * E.B * ((double)Sq * C * 2 + (double)Sk * C * 2);
-    char kern[32];
-    snprintf(kern, sizeof kern, "attn_d%d", C / kHeads);
     char shape[64];
     snprintf(shape, sizeof shape, "Sq=%d Sk=%d d=%d", Sq, Sk, C / kHeads);
-    E.run(cat, kern, flops, bytes, [&] { return attention_launch(a, E.s); }, shape);
+    E.run(cat, [&] { return attention_launch(a, E.s); }, shape);
 }
 
 // ------------------------------------------------------------------ blocks
@@ -154,7 +161,7 @@ static f16* resnet(Exec& E, const ResDesc& r, const f16* x, const f16* x2, int H
         GemmArgs a = conv3_args(h, B, H, Wd, r.cin, r.cout, 1, 0, W(E, r.pf + ".conv1.weight"), hc);
         a.bias = W(E, r.pf + ".conv1.bias");
         a.bias2 = tproj + r.tproj_off;  // + time_emb_proj(silu(temb)) broadcast (:627-630)
-        gemm(E, "conv3x3", a, 2.0 * M * r.cout * 9.0 * r.cin);
+        gemm(E, "conv3x3", a);
     }
     f16* h2 = E.alloc<f16>((size_t)M * r.cout);
     groupnorm(E, hc, nullptr, r.cout, 0, W(E, r.pf + ".norm2.weight"), W(E, r.pf + ".norm2.bias"), h2,
@@ -165,14 +172,14 @@ static f16* resnet(Exec& E, const ResDesc& r, const f16* x, const f16* x2, int H
         GemmArgs a = dense_args(x, r.cin1, M, r.cout, r.cin, W(E, r.pf + ".conv_shortcut.weight"), sx, r.cout);
         if (x2) { a.A2 = x2; a.lda2 = r.cin - r.cin1; a.K1 = r.cin1; }
         a.bias = W(E, r.pf + ".conv_shortcut.bias");
-        gemm(E, "conv1x1", a, 2.0 * M * r.cout * r.cin);
+        gemm(E, "conv1x1", a);
         res = sx;
     }
     {
         GemmArgs a = conv3_args(h2, B, H, Wd, r.cout, r.cout, 1, 0, W(E, r.pf + ".conv2.weight"), out);
         a.bias = W(E, r.pf + ".conv2.bias");
         a.res = res; a.ldr = r.cout;
-        gemm(E, "conv3x3", a, 2.0 * M * r.cout * 9.0 * r.cout);
+        gemm(E, "conv3x3", a);
     }
     E.ar->release(mk);
     return out;
@@ -190,32 +197,31 @@ static f16* transformer(Exec& E, const XfDesc& t, const f16* x, int H, int Wd, c
     {
         GemmArgs a = dense_args(g, C, M, C, C, W(E, t.pf + ".proj_in.weight"), tt, C);
         a.bias = W(E, t.pf + ".proj_in.bias");
-        gemm(E, "conv1x1", a, 2.0 * M * C * C);
+        gemm(E, "conv1x1", a);
     }
     f16* h = E.alloc<f16>((size_t)M * C);
     f16* qkv = E.alloc<f16>((size_t)M * 3 * C);
     f16* at = E.alloc<f16>((size_t)M * C);
     // self-attention
     layernorm(E, tt, W(E, b + ".norm1.weight"), W(E, b + ".norm1.bias"), h, M, C);
-    gemm(E, "linear", dense_args(h, C, M, 3 * C, C, W(E, b + ".attn1.to_q.weight"), qkv, 3 * C),
-         2.0 * M * 3 * C * C);
+    gemm(E, "linear", dense_args(h, C, M, 3 * C, C, W(E, b + ".attn1.to_q.weight"), qkv, 3 * C));
     attention(E, "attn_self", qkv, qkv + C, qkv + 2 * C, at, HW, HW, C, 3 * C, 3 * C, 3 * C);
     {
         GemmArgs a = dense_args(at, C, M, C, C, W(E, b + ".attn1.to_out.0.weight"), tt, C);
         a.bias = W(E, b + ".attn1.to_out.0.bias");
         a.res = tt; a.ldr = C;
-        gemm(E, "linear", a, 2.0 * M * C * C);
+        gemm(E, "linear", a);
     }
     // cross-attention: K/V of this block are columns [kv_off, kv_off + 2C) of kv
     layernorm(E, tt, W(E, b + ".norm2.weight"), W(E, b + ".norm2.bias"), h, M, C);
-    gemm(E, "linear", dense_args(h, C, M, C, C, W(E, b + ".attn2.to_q.weight"), qkv, C), 2.0 * M * C * C);
+    gemm(E, "linear", dense_args(h, C, M, C, C, W(E, b + ".attn2.to_q.weight"), qkv, C));
     const int ldkv = E.c.kv_total;
     attention(E, "attn_cross", qkv, kv + t.kv_off, kv + t.kv_off + C, at, HW, L, C, C, ldkv, ldkv);
     {
         GemmArgs a = dense_args(at, C, M, C, C, W(E, b + ".attn2.to_out.0.weight"), tt, C);
         a.bias = W(E, b + ".attn2.to_out.0.bias");
         a.res = tt; a.ldr = C;
-        gemm(E, "linear", a, 2.0 * M * C * C);
+        gemm(E, "linear", a);
     }
     // GEGLU feed-forward: proj (+bias, GEGLU in the epilogue) then out (+bias, +residual)
     layernorm(E, tt, W(E, b + ".norm3.weight"), W(E, b + ".norm3.bias"), h, M, C);
@@ -224,19 +230,19 @@ static f16* transformer(Exec& E, const XfDesc& t, const f16* x, int H, int Wd, c
         GemmArgs a = dense_args(h, C, M, 8 * C, C, W(E, b + ".ff.net.0.proj.weight"), ff, 4 * C);
         a.bias = W(E, b + ".ff.net.0.proj.bias");
         a.geglu = 1;
-        gemm(E, "linear_geglu", a, 2.0 * M * 8 * C * C);
+        gemm(E, "linear_geglu", a);
     }
     {
         GemmArgs a = dense_args(ff, 4 * C, M, C, 4 * C, W(E, b + ".ff.net.2.weight"), tt, C);
         a.bias = W(E, b + ".ff.net.2.bias");
         a.res = tt; a.ldr = C;
-        gemm(E, "linear", a, 2.0 * M * C * 4 * C);
+        gemm(E, "linear", a);
     }
     {
         GemmArgs a = dense_args(tt, C, M, C, C, W(E, t.pf + ".proj_out.weight"), out, C);
         a.bias = W(E, t.pf + ".proj_out.bias");
         a.res = x; a.ldr = C;
-        gemm(E, "conv1x1", a, 2.0 * M * C * C);
+        gemm(E, "conv1x1", a);
     }
     E.ar->release(mk);
     return out;
@@ -248,7 +254,7 @@ static f16* conv3_block(Exec& E, const std::string& pf, const f16* x, int H, int
     f16* y = E.alloc<f16>((size_t)a.M * Cout);
     a.C = y;
     a.bias = W(E, pf + ".bias");
-    gemm(E, "conv3x3", a, 2.0 * a.M * Cout * 9.0 * Cin);
+    gemm(E, "conv3x3", a);
     return y;
 }
 
@@ -259,15 +265,15 @@ static float* time_embed(Exec& E, const float* temb320) {
     float* t1 = E.alloc<float>(1280);
     float* temb = E.alloc<float>(1280);
     float* tproj = E.alloc<float>(c.tproj_total);
-    E.run("time_mlp", "gemv", 2.0 * 1280 * 320, 2.0 * 1280 * 320, [&] {
+    E.run("time_mlp", [&] {
         return gemv_launch(temb320, c.wd("time_embedding.linear_1.weight"), c.wd("time_embedding.linear_1.bias"),
                            t1, 1280, 320, 0, 1, E.s);
     });
-    E.run("time_mlp", "gemv", 2.0 * 1280 * 1280, 2.0 * 1280 * 1280, [&] {
+    E.run("time_mlp", [&] {
         return gemv_launch(t1, c.wd("time_embedding.linear_2.weight"), c.wd("time_embedding.linear_2.bias"),
                            temb, 1280, 1280, 0, 0, E.s);
     });
-    E.run("time_mlp", "gemv", 2.0 * c.tproj_total * 1280, 2.0 * c.tproj_total * 1280, [&] {
+    E.run("time_mlp", [&] {
         return gemv_launch(temb, c.w_tproj, c.b_tproj, tproj, c.tproj_total, 1280, 1, 0, E.s);
     });
     return tproj;
@@ -278,8 +284,7 @@ static f16* cross_kv(Exec& E, const f16* ctx16, int L) {
     Ctx& c = E.c;
     const int M = E.B * L;
     f16* kv = E.alloc<f16>((size_t)M * c.kv_total);
-    gemm(E, "cross_kv", dense_args(ctx16, kCtxDim, M, c.kv_total, kCtxDim, c.w_kv, kv, c.kv_total),
-         2.0 * M * c.kv_total * kCtxDim);
+    gemm(E, "cross_kv", dense_args(ctx16, kCtxDim, M, c.kv_total, kCtxDim, c.w_kv, kv, c.kv_total));
     return kv;
 }
 
@@ -294,7 +299,7 @@ static void unet_core(Exec& E, const Fwd& F, const f16* lat, const float* temb32
     E.gn_acc = E.alloc<double>(acc_bytes / sizeof(double));
     {
         void* p = E.gn_acc;
-        E.run("groupnorm", "zero", 0, (double)acc_bytes, [&] { return zero_launch(p, acc_bytes, E.s); });
+        E.run("groupnorm", [&] { return zero_launch(p, acc_bytes, E.s); });
     }
     const float* tproj = time_embed(E, temb320);
     int H = F.H, Wd = F.W;
@@ -355,7 +360,7 @@ static void unet_core(Exec& E, const Fwd& F, const f16* lat, const float* temb32
     a.out_mode = OUT_F32_NCHW;
     a.ldc = kLatC;
     a.hw_out = H * Wd;
-    gemm(E, "conv3x3", a, 2.0 * M * kLatC * 9.0 * 320);
+    gemm(E, "conv3x3", a);
     E.ar->release(mk0);
 }
 
@@ -432,8 +437,8 @@ static void body(Exec& E, FwdState& S) {
     if (S.kind == 0) {
         f16* lat = E.alloc<f16>((size_t)F.B * HW * kLatCpad);
         f16* ctx16 = E.alloc<f16>((size_t)F.B * F.L * kCtxDim);
-        E.run("io", "convert", 0, 0, [&] { return nchw_to_nhwc_launch(S.in_lat, lat, F.B, F.B, kLatC, kLatCpad, HW, E.s); });
-        E.run("io", "convert", 0, 0, [&] { return f32_to_f16_launch(S.in_ctx, ctx16, (int64_t)F.B * F.L * kCtxDim, E.s); });
+        E.run("io", [&] { return nchw_to_nhwc_launch(S.in_lat, lat, F.B, F.B, kLatC, kLatCpad, HW, E.s); });
+        E.run("io", [&] { return f32_to_f16_launch(S.in_ctx, ctx16, (int64_t)F.B * F.L * kCtxDim, E.s); });
         const f16* kv = cross_kv(E, ctx16, F.L);
         unet_core(E, F, lat, S.in_temb, kv, S.out);
         return;
@@ -443,12 +448,12 @@ static void body(Exec& E, FwdState& S) {
     f16* lat = E.alloc<f16>((size_t)2 * HW * kLatCpad);
     f16* ctx16 = E.alloc<f16>((size_t)2 * F.L * kCtxDim);
     float* eps2 = E.alloc<float>((size_t)2 * n);
-    E.run("io", "convert", 0, 0, [&] {
+    E.run("io", [&] {
         hipError_t e = hipMemcpyAsync(S.out, S.in_lat, n * sizeof(float), hipMemcpyDeviceToDevice, E.s);
         if (e != hipSuccess) return e;
         return nchw_to_nhwc_launch(S.in_lat, lat, 2, 1, kLatC, kLatCpad, HW, E.s);
     });
-    E.run("io", "convert", 0, 0, [&] { return f32_to_f16_launch(S.in_ctx, ctx16, (int64_t)2 * F.L * kCtxDim, E.s); });
+    E.run("io", [&] { return f32_to_f16_launch(S.in_ctx, ctx16, (int64_t)2 * F.L * kCtxDim, E.s); });
     const f16* kv = cross_kv(E, ctx16, F.L);  // context is fixed across steps
     LcmSched sched(S.steps);
     for (int i = 0; i < S.steps; ++i) {
@@ -456,7 +461,7 @@ static void body(Exec& E, FwdState& S) {
         const LcmCoeffs co = sched.coeffs(i, S.guidance);
         const float* nz = co.last ? nullptr : S.in_noise + (size_t)i * n;
         f16* next = co.last ? nullptr : lat;
-        E.run("lcm_step", "lcm_step", 0, 4.0 * n * 5, [&] {
+        E.run("lcm_step", [&] {
             return lcm_step_launch(S.out, eps2, nz, n, co, next, kLatC, HW, kLatCpad, E.s);
         });
     }
@@ -616,7 +621,11 @@ int unet_denoise_device(Ctx& c, const float* d_lat, const float* d_cond, const f
     return SDU_OK;
 }
 
-// Eager forward with per-kernel HIP events (unetProfile, vk_engine.cpp:854-872).
+// Eager forward with every kernel timed on its own (unetProfile,
+// vk_engine.cpp:854-872).  Each launch is repeated SDU_PROFILE_REPS times (default
+// 5) between its two events; the recorded time is the per-launch average.  The
+// repeats recompute the same kernels on the same buffers, so the activations of
+// this pass are not meaningful; the next forward starts from its own inputs.
 int unet_profile(Ctx& c, int B, int H, int W, int L) {
     int st = check_shape(c, B, H, W, L);
     if (st) return st;
@@ -627,23 +636,33 @@ int unet_profile(Ctx& c, int B, int H, int W, int L) {
     Arena ar;
     ar.base = S->arena;
     ar.cap = S->arena_bytes;
-    std::vector<ProfRec> recs;
+    EventTimer timer;
+    timer.s = c.stream;
+    if (const char* r = getenv("SDU_PROFILE_REPS")) timer.reps = std::min(100, std::max(1, atoi(r)));
     Exec E{c, c.stream, &ar, B};
     E.gemm_ws = S->gemm_ws;
-    E.prof = &recs;
-    body(E, *S);
+    E.timer = &timer;
+    struct Install {
+        explicit Install(KernelTimer* t) { g_kernel_timer = t; }
+        ~Install() { g_kernel_timer = nullptr; }
+    };
+    {
+        Install guard(&timer);
+        body(E, *S);
+    }
     e = hipStreamSynchronize(c.stream);
     if (E.err != hipSuccess) e = E.err;
     c.prof.clear();
-    // SDU_PROFILE_DUMP=<path>: also write one CSV line per launch
+    // SDU_PROFILE_DUMP=<path>: also write one CSV line per kernel launch
     FILE* dump = nullptr;
     if (const char* path = getenv("SDU_PROFILE_DUMP")) {
         dump = fopen(path, "w");
         if (dump) fprintf(dump, "category,kernel,shape,flops,bytes,ms\n");
     }
-    for (ProfRec& r : recs) {
+    for (ProfRec& r : timer.recs) {
         float ms = 0.f;
         if (e == hipSuccess) hipEventElapsedTime(&ms, r.e0, r.e1);
+        ms /= (float)r.reps;
         hipEventDestroy(r.e0);
         hipEventDestroy(r.e1);
         if (dump) fprintf(dump, "%s,%s,%s,%.0f,%.0f,%.5f\n", r.cat.c_str(), r.kern.c_str(), r.shape.c_str(),

@@ -51,7 +51,7 @@ class SduError(RuntimeError):
 
 
 class ProfEntry(ctypes.Structure):
-    _fields_ = [("name", ctypes.c_char * 32), ("calls", ctypes.c_int), ("ms", ctypes.c_double),
+    _fields_ = [("name", ctypes.c_char * 48), ("calls", ctypes.c_int), ("ms", ctypes.c_double),
                 ("flops", ctypes.c_double), ("bytes", ctypes.c_double)]
 
 
