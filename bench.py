@@ -125,6 +125,16 @@ def main():
     out = d_out.numpy()
     assert np.isfinite(out).all(), "non-finite UNet output"
 
+    # the same forward through the host-buffer entry point (sdu_forward: pageable host
+    # inputs and output, copies over PCIe included) -- reported beside `value`, never as it
+    for _ in range(3):
+        eng.forward(lat, temb, ctx)
+    t0 = time.perf_counter()
+    host_reps = max(5, args.steps // 5)
+    for _ in range(host_reps):
+        eng.forward(lat, temb, ctx)
+    host_fps = host_reps / (time.perf_counter() - t0)
+
     # 4-step LCM + CFG denoise (guidance 8), device-resident
     steps = 4
     lat1 = weights.gauss("input.latent", (4, H, W), 2, fp16=False)
@@ -198,6 +208,7 @@ def main():
         "config": {"workload": "SD1.5 UNet forward, batch-CFG B=2, 2x4x64x64 latent, 2x77x768 context",
                    "global_batch": B, "latent": [H, W], "context_tokens": L, "parallelism": "single GPU"},
         "lcm_4step_ms": round(lcm_ms, 3),
+        "host_io_forwards_per_s": round(host_fps, 3),
         "roofline": roof,
         "cpu_baseline": cpu,
         "profile_total_ms": round(prof_total, 4),
