@@ -10,17 +10,32 @@
 // 8-11 in every 16) so that each lane's score registers are directly the B
 // operand of O^T = V^T . P^T, again 32x32x16 with lane l owning query l%32: the
 // online-softmax rescale is a per-lane scalar and no cross-lane shuffles are
-// needed except one max / sum exchange with lane l^32.  V is staged transposed
-// in LDS ([dim][key]) so the A operand is one 16-byte read.
+// needed except one max exchange with lane l^32.  V is staged transposed in LDS
+// ([dim][key]) so the A operand is one 16-byte read.
+//
+// Softmax cost per score: one FMA (scale and max folded), one v_exp_f32, a third
+// of a v_max3 and half a packed convert.  The running max is only moved when a
+// tile raises it by more than 2^8 (wave-uniform branch), so P = 2^(s*c - m) stays
+// <= 256, exact in fp16 and far from overflow, and the O rescale is skipped on
+// almost every tile.  When the head size leaves a spare row in the last 32-row
+// dim tile, that row of V^T is set to 1 so the PV MFMA also produces the row sums.
+//
+// Two kernels:
+//   attn_kernel       -- NWAVE query waves share each 64-key K/V tile in LDS
+//                        (long sequences: 64x64 self-attention, 4096 tokens);
+//   attn_split_kernel -- NSPLIT waves split the keys of one 32-query group and
+//                        merge their partial (max, sum, O) through LDS (short query
+//                        counts, where one wave per 32 queries cannot fill the chip).
 #include "sdu_internal.h"
+
+#include <cstdio>
 
 namespace sdu {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-static constexpr int KT = 64;        // keys per iteration
-static constexpr int VSTR = KT + 8;  // Vt row stride (halves)
+static constexpr float kRescaleLog2 = 8.0f;  // lazy-rescale threshold (log2 units)
 
 __device__ __forceinline__ int key_perm(int r) {
     const int o = r & 15;
@@ -28,9 +43,90 @@ __device__ __forceinline__ int key_perm(int r) {
     return (r & ~15) | po;
 }
 
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Online-softmax update for NSUB 32-key sub-tiles of raw scores s (S^T layout)
+// followed by O^T += V^T . P^T.  `kvalid` = number of valid keys in the tile
+// (< NSUB*32 only on the last tile).  vt: V^T tile [dim][key] with row stride vstr.
+template <int NSUB, int MTD, bool LSUM>
+__device__ __forceinline__ void softmax_pv(floatx16 (&s)[NSUB], int kvalid, float c, float& m_run,
+                                           float& l_run, floatx16 (&o)[MTD], const f16* vt, int vstr,
+                                           int hl, int lrow, int lk) {
+    if (kvalid < NSUB * 32) {
+#pragma unroll
+        for (int sub = 0; sub < NSUB; ++sub)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int key = sub * 32 + key_perm((e >> 2) * 8 + hl * 4 + (e & 3));
+                if (key >= kvalid) s[sub][e] = -INFINITY;
+            }
+    }
+    float mx = s[0][0];
+#pragma unroll
+    for (int sub = 0; sub < NSUB; ++sub)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[sub][e]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mxs = mx * c;
+    if (__ballot(mxs > m_run + kRescaleLog2)) {  // wave-uniform
+        const float m_new = fmaxf(m_run, mxs);
+        const float alpha = fast_exp2(m_run - m_new);  // m_run = -inf on the first tile -> 0
+#pragma unroll
+        for (int t = 0; t < MTD; ++t) o[t] *= alpha;
+        l_run *= alpha;
+        m_run = m_new;
+    }
+    const float nm = -m_run;
+    float psum = 0.f;
+#pragma unroll
+    for (int sub = 0; sub < NSUB; ++sub)
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            half8 pf;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float p = fast_exp2(__builtin_fmaf(s[sub][st * 8 + i], c, nm));
+                if (!LSUM) psum += p;
+                pf[i] = (f16)p;
+            }
+            const int kofs = sub * 32 + st * 16 + lk;
+#pragma unroll
+            for (int t = 0; t < MTD; ++t) {
+                const half8 vf = *(const half8*)&vt[(t * 32 + lrow) * vstr + kofs];
+                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, o[t], 0, 0, 0);
+            }
+        }
+    if (!LSUM) l_run += psum;
+}
+
+// Row sum of P for query lrow at the end: from the ones row of V^T (LSUM: dim
+// MTD*32-1 = register 15 of the last dim tile on lanes 32..63) or from the
+// per-lane partial sums.
+template <int MTD, bool LSUM>
+__device__ __forceinline__ float row_sum(const floatx16 (&o)[MTD], float l_run, int lrow) {
+    if (LSUM) return __shfl(o[MTD - 1][15], lrow + 32);
+    return l_run + __shfl_xor(l_run, 32);
+}
+
+// Set rows [d, MTD*32) of a V^T tile of `keys` columns: zero, and the last one to 1
+// when LSUM.  Rows below d are written per tile and never touch these.
+template <int MTD, bool LSUM>
+__device__ __forceinline__ void vt_pad_rows(f16* vt, int vstr, int keys, int d, int tid, int nth) {
+    const int rows = MTD * 32 - d;
+    for (int i = tid; i < rows * keys; i += nth) {
+        const int dim = d + i / keys, key = i % keys;
+        vt[dim * vstr + key] = (f16)((LSUM && dim == MTD * 32 - 1) ? 1.f : 0.f);
+    }
+}
+
+// ----------------------------------------------------------------- shared-tile kernel
+
+static constexpr int KT = 64;        // keys per iteration
+static constexpr int VSTR = KT + 8;  // Vt row stride (halves)
+
 // KS: 16-wide k-steps covering d for QK^T; MTD: 32-row dim tiles for PV;
 // NWAVE: waves per block (32 queries each; they share the K/V tiles in LDS).
-template <int KS, int MTD, int NWAVE>
+template <int KS, int MTD, int NWAVE, bool LSUM>
 __global__ __launch_bounds__(NWAVE * 64) void attn_kernel(AttnArgs a) {
     constexpr int KSTR = KS * 16 + 8;  // K row stride (halves)
     constexpr int NTH = NWAVE * 64;
@@ -44,11 +140,14 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_kernel(AttnArgs a) {
     const int lrow = lane & 31, hl = lane >> 5, lk = hl * 8;
     const float c = a.scale * 1.4426950408889634f;
 
-    // zero the K padding columns [d, KS*16) of both buffers (never overwritten)
+    // zero the K padding columns [d, KS*16) of both buffers and set the V^T pad rows
+    // (never overwritten by the tile stores)
     for (int i = tid; i < 2 * KT; i += NTH) {
         f16* row = &Ks[i / KT][(i % KT) * KSTR];
         for (int x = d; x < KS * 16; ++x) row[x] = (f16)0.f;
     }
+    vt_pad_rows<MTD, LSUM>(Vt[0], VSTR, KT, d, tid, NTH);
+    vt_pad_rows<MTD, LSUM>(Vt[1], VSTR, KT, d, tid, NTH);
 
     // Q fragment (B operand of S^T = K Q^T): lane holds Q[q0+lrow][ks*16+lk .. +7]
     half8 qf[KS];
@@ -108,7 +207,7 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_kernel(AttnArgs a) {
 
     const int nt = (a.Sk + KT - 1) / KT;
     load_kv(0);
-    __syncthreads();  // padding zeroed before the first K stores land next to it
+    __syncthreads();  // padding set before the first tile stores land next to it
     store_kv(0);
     __syncthreads();
 
@@ -128,55 +227,12 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_kernel(AttnArgs a) {
                 s[sub] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], s[sub], 0, 0, 0);
             }
         }
-        // scale into the log2 domain, mask keys >= Sk, tile max
-        float mx = -INFINITY;
-#pragma unroll
-        for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int r = (e >> 2) * 8 + hl * 4 + (e & 3);
-                const int key = kb + sub * 32 + key_perm(r);
-                const float v = (key < a.Sk) ? s[sub][e] * c : -INFINITY;
-                s[sub][e] = v;
-                mx = fmaxf(mx, v);
-            }
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float m_new = fmaxf(m_run, mx);
-        const float alpha = exp2f(m_run - m_new);  // m_run = -inf on the first tile -> 0
-        float psum = 0.f;
-        half8 pf[2][2];
-#pragma unroll
-        for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-            for (int st = 0; st < 2; ++st)
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const float p = exp2f(s[sub][st * 8 + i] - m_new);
-                    psum += p;
-                    pf[sub][st][i] = (f16)p;
-                }
-        l_run = l_run * alpha + psum;
-        m_run = m_new;
-#pragma unroll
-        for (int t = 0; t < MTD; ++t) o[t] *= alpha;
-        // O^T += V^T . P^T over the 64 keys (4 k-steps of 16)
-#pragma unroll
-        for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-            for (int st = 0; st < 2; ++st) {
-                const int kofs = sub * 32 + st * 16 + lk;
-#pragma unroll
-                for (int t = 0; t < MTD; ++t) {
-                    const half8 vf = *(const half8*)&Vt[buf][(t * 32 + lrow) * VSTR + kofs];
-                    o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[sub][st], o[t], 0, 0, 0);
-                }
-            }
+        softmax_pv<2, MTD, LSUM>(s, min(KT, a.Sk - kb), c, m_run, l_run, o, Vt[buf], VSTR, hl, lrow, lk);
         if (it + 1 < nt) store_kv(buf ^ 1);
         __syncthreads();
     }
 
-    const float l_tot = l_run + __shfl_xor(l_run, 32);
-    const float inv = 1.0f / l_tot;
+    const float inv = 1.0f / row_sum<MTD, LSUM>(o, l_run, lrow);
     const int q = q0 + lrow;
     if (q < a.Sq) {
         f16* op = a.o + ((int64_t)b * a.Sq + q) * a.ldo + (int64_t)h * d;
@@ -190,41 +246,212 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_kernel(AttnArgs a) {
     }
 }
 
-// MINNW: the smallest block a head size may use (one-wave blocks at d > 96 would
-// need more registers for the K/V prefetch than a wave has).
-template <int KS, int MTD, int MINNW>
-static void launch_nw(const AttnArgs& a, int nw, hipStream_t s) {
-    const dim3 grid4((a.Sq + 127) / 128, a.heads, a.B), grid2((a.Sq + 63) / 64, a.heads, a.B),
-        grid1((a.Sq + 31) / 32, a.heads, a.B);
-    if (nw < 2 && MINNW > 1) nw = 2;
-    char name[32];
-    snprintf(name, sizeof name, "attn_kernel<%d,%d,%d>", KS, MTD, nw);
-    // algorithmic work: QK^T and PV at the true head size; Q, K, V read and O written once
-    const double bh = (double)a.B * a.heads;
+// ----------------------------------------------------------------- key-split kernel
+
+static constexpr int KTS = 32;         // keys per step
+static constexpr int VSTRS = KTS + 8;  // per-wave Vt row stride (halves)
+
+template <int MTD, int NSPLIT>
+struct SplitSmem {
+    static constexpr int vt_bytes = NSPLIT * MTD * 32 * VSTRS * 2;
+    static constexpr int comb_bytes = NSPLIT * (MTD * 32 * 32 + 64) * 4;
+    static constexpr int bytes = vt_bytes > comb_bytes ? vt_bytes : comb_bytes;
+};
+
+// One block = one group of 32 queries of one (image, head); wave w handles key
+// tiles w, w+NSPLIT, ...  K fragments come straight from global memory (each lane
+// reads 16 contiguous bytes of one key row); V goes through a per-wave transposed
+// LDS tile.  Within a wave LDS operations complete in order, so the per-wave tile
+// needs no block barrier; one barrier separates the key loop from the merge.
+template <int KS, int MTD, int NSPLIT, bool LSUM>
+__global__ __launch_bounds__(NSPLIT * 64) void attn_split_kernel(AttnArgs a) {
+    constexpr int NTH = NSPLIT * 64;
+    __shared__ __attribute__((aligned(16))) char smem[SplitSmem<MTD, NSPLIT>::bytes];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int h = blockIdx.y, b = blockIdx.z;
+    const int d = a.d, dch = d >> 3;
+    const int q0 = blockIdx.x * 32;
+    const int lrow = lane & 31, hl = lane >> 5, lk = hl * 8;
+    const float c = a.scale * 1.4426950408889634f;
+    f16* vt = (f16*)smem + wave * (MTD * 32 * VSTRS);
+
+    vt_pad_rows<MTD, LSUM>(vt, VSTRS, KTS, d, lane, 64);
+
+    half8 qf[KS];
+    {
+        const int q = q0 + lrow;
+        const f16* qp = a.q + ((int64_t)b * a.Sq + q) * a.ldq + (int64_t)h * d;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const int dd = ks * 16 + lk;
+            half8 v = {};
+            if (q < a.Sq && dd < d) v = *(const half8*)(qp + dd);
+            qf[ks] = v;
+        }
+    }
+
+    floatx16 o[MTD];
+#pragma unroll
+    for (int t = 0; t < MTD; ++t) o[t] = floatx16{};
+    float m_run = -INFINITY, l_run = 0.f;
+
+    const f16* kbase = a.k + (int64_t)b * a.Sk * a.ldk + (int64_t)h * d;
+    const f16* vbase = a.v + (int64_t)b * a.Sk * a.ldv + (int64_t)h * d;
+    constexpr int MAXCH = (KTS * KS * 2 + 63) / 64;  // V chunks per lane per tile
+    const int nchunk = KTS * dch;
+    half8 kf[KS];
+    uint4 rv[MAXCH];
+
+    auto load = [&](int kb) {
+        const int key = kb + key_perm(lrow);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const int dd = ks * 16 + lk;
+            half8 v = {};
+            if (key < a.Sk && dd < d) v = *(const half8*)(kbase + (int64_t)key * a.ldk + dd);
+            kf[ks] = v;
+        }
+#pragma unroll
+        for (int i = 0; i < MAXCH; ++i) {
+            const int cidx = lane + i * 64;
+            uint4 vv = make_uint4(0, 0, 0, 0);
+            if (cidx < nchunk) {
+                const int kk = cidx / dch, dc = cidx - kk * dch;
+                if (kb + kk < a.Sk) vv = *(const uint4*)(vbase + (int64_t)(kb + kk) * a.ldv + dc * 8);
+            }
+            rv[i] = vv;
+        }
+    };
+    auto store_v = [&]() {
+#pragma unroll
+        for (int i = 0; i < MAXCH; ++i) {
+            const int cidx = lane + i * 64;
+            if (cidx < nchunk) {
+                const int kk = cidx / dch, dc = cidx - kk * dch;
+                const f16* vh = (const f16*)&rv[i];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) vt[(dc * 8 + e) * VSTRS + kk] = vh[e];
+            }
+        }
+    };
+
+    const int ntile = (a.Sk + KTS - 1) / KTS;
+    for (int it = wave; it < ntile; it += NSPLIT) {
+        const int kb = it * KTS;
+        load(kb);
+        store_v();
+        __builtin_amdgcn_wave_barrier();
+        floatx16 s[1];
+        s[0] = floatx16{};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+            s[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[ks], qf[ks], s[0], 0, 0, 0);
+        softmax_pv<1, MTD, LSUM>(s, min(KTS, a.Sk - kb), c, m_run, l_run, o, vt, VSTRS, hl, lrow, lk);
+        __builtin_amdgcn_wave_barrier();
+    }
+
+    // merge: per wave (max, sum) per query and O^T partials [dim][query] in fp32
+    const float l_tot = row_sum<MTD, LSUM>(o, l_run, lrow);
+    __syncthreads();  // every wave is done with its V^T tile
+    float* Ow = (float*)smem;                       // [NSPLIT][MTD*32][32]
+    float* Mw = Ow + NSPLIT * MTD * 32 * 32;        // [NSPLIT][32]
+    float* Lw = Mw + NSPLIT * 32;                   // [NSPLIT][32]
+#pragma unroll
+    for (int t = 0; t < MTD; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int dim = t * 32 + (e >> 2) * 8 + hl * 4 + (e & 3);
+            Ow[(wave * MTD * 32 + dim) * 32 + lrow] = o[t][e];
+        }
+    if (hl == 0) {
+        Mw[wave * 32 + lrow] = m_run;
+        Lw[wave * 32 + lrow] = l_tot;
+    }
+    __syncthreads();
+    // each thread produces 8 consecutive dims of one query
+    const int nch = 32 * dch;
+    for (int i = tid; i < nch; i += NTH) {
+        const int q = i & 31, dc = i >> 5;
+        if (q0 + q >= a.Sq) continue;
+        float mmax = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NSPLIT; ++w) mmax = fmaxf(mmax, Mw[w * 32 + q]);
+        float wt[NSPLIT], lsum = 0.f;
+#pragma unroll
+        for (int w = 0; w < NSPLIT; ++w) {
+            wt[w] = fast_exp2(Mw[w * 32 + q] - mmax);  // an idle wave: -inf -> 0
+            lsum += wt[w] * Lw[w * 32 + q];
+        }
+        const float inv = 1.0f / lsum;
+        uint4 outv;
+        f16* ov = (f16*)&outv;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float acc = 0.f;
+#pragma unroll
+            for (int w = 0; w < NSPLIT; ++w) acc += wt[w] * Ow[(w * MTD * 32 + dc * 8 + e) * 32 + q];
+            ov[e] = (f16)(acc * inv);
+        }
+        *(uint4*)(a.o + ((int64_t)b * a.Sq + q0 + q) * a.ldo + (int64_t)h * d + dc * 8) = outv;
+    }
+}
+
+// ----------------------------------------------------------------- launch
+
+template <int KS, int MTD, bool LSUM>
+static void launch_cfg(const AttnArgs& a, hipStream_t s) {
+    const int64_t bh = (int64_t)a.heads * a.B;
+    const int64_t qwaves = ((a.Sq + 31) / 32) * bh;  // one wave per 32 queries
     const double flops = 4.0 * bh * a.Sq * a.Sk * a.d;
     const double bytes = 2.0 * bh * a.d * (2.0 * a.Sq + 2.0 * a.Sk);
+    char name[48];
+    if (qwaves >= 1024) {
+        // shared K/V tiles; two waves per block when four would leave < 512 blocks
+        const int nw = ((a.Sq + 127) / 128) * bh >= 512 ? 4 : 2;
+        snprintf(name, sizeof name, "attn_kernel<%d,%d,%d,%d>", KS, MTD, nw, (int)LSUM);
+        const dim3 grid((a.Sq + nw * 32 - 1) / (nw * 32), a.heads, a.B);
+        launch_timed(name, flops, bytes, [&] {
+            if (nw == 4) hipLaunchKernelGGL((attn_kernel<KS, MTD, 4, LSUM>), grid, dim3(256), 0, s, a);
+            else hipLaunchKernelGGL((attn_kernel<KS, MTD, 2, LSUM>), grid, dim3(128), 0, s, a);
+        });
+        return;
+    }
+    // key split: enough waves to fill the chip, at most one per 32-key tile, and at
+    // most 4 for wide heads (LDS for the fp32 merge)
+    const int ntile = (a.Sk + KTS - 1) / KTS;
+    int ns = (int)((2048 + qwaves - 1) / qwaves);
+    if (ns > ntile) ns = ntile;
+    const int nmax = MTD > 3 ? 4 : 8;
+    ns = ns <= 1 ? 1 : ns <= 2 ? 2 : (ns <= 4 || nmax == 4) ? 4 : 8;
+    snprintf(name, sizeof name, "attn_split_kernel<%d,%d,%d,%d>", KS, MTD, ns, (int)LSUM);
+    const dim3 grid((a.Sq + 31) / 32, a.heads, a.B);
     launch_timed(name, flops, bytes, [&] {
-        if (nw == 4) hipLaunchKernelGGL((attn_kernel<KS, MTD, 4>), grid4, dim3(256), 0, s, a);
-        else if (nw == 2) hipLaunchKernelGGL((attn_kernel<KS, MTD, 2>), grid2, dim3(128), 0, s, a);
-        else hipLaunchKernelGGL((attn_kernel<KS, MTD, MINNW>), grid1, dim3(64 * MINNW), 0, s, a);
+        if (ns == 1) hipLaunchKernelGGL((attn_split_kernel<KS, MTD, 1, LSUM>), grid, dim3(64), 0, s, a);
+        else if (ns == 2) hipLaunchKernelGGL((attn_split_kernel<KS, MTD, 2, LSUM>), grid, dim3(128), 0, s, a);
+        else if (ns == 4) hipLaunchKernelGGL((attn_split_kernel<KS, MTD, 4, LSUM>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((attn_split_kernel<KS, MTD, (MTD > 3 ? 4 : 8), LSUM>), grid,
+                                dim3(64 * (MTD > 3 ? 4 : 8)), 0, s, a);
     });
 }
 
+template <int KS, int MTD>
+static void launch_d(const AttnArgs& a, hipStream_t s) {
+    if (a.d < MTD * 32) launch_cfg<KS, MTD, true>(a, s);
+    else launch_cfg<KS, MTD, false>(a, s);
+}
+
 hipError_t attention_launch(const AttnArgs& a, hipStream_t s) {
-    if (a.d <= 0 || a.d > 160 || (a.d & 7) || a.Sq <= 0 || a.Sk <= 0) return hipErrorInvalidValue;
-    // fewer waves per block when the query count alone would not fill the chip
-    const int64_t bh = (int64_t)a.heads * a.B;
-    int nw = 4;
-    if (((a.Sq + 127) / 128) * bh < 512) nw = 2;
-    if (nw == 2 && ((a.Sq + 63) / 64) * bh < 512) nw = 1;
+    if (a.d <= 0 || a.d > 160 || (a.d & 7) || a.Sq <= 0 || a.Sk <= 0 || !(a.scale > 0.f))
+        return hipErrorInvalidValue;
     const int d = a.d;
-    if (d <= 32) launch_nw<2, 1, 1>(a, nw, s);
-    else if (d <= 48) launch_nw<3, 2, 1>(a, nw, s);
-    else if (d <= 64) launch_nw<4, 2, 1>(a, nw, s);
-    else if (d <= 80) launch_nw<5, 3, 1>(a, nw, s);
-    else if (d <= 96) launch_nw<6, 3, 1>(a, nw, s);
-    else if (d <= 128) launch_nw<8, 4, 2>(a, nw, s);
-    else launch_nw<10, 5, 2>(a, nw, s);
+    if (d <= 32) launch_d<2, 1>(a, s);
+    else if (d <= 48) launch_d<3, 2>(a, s);
+    else if (d <= 64) launch_d<4, 2>(a, s);
+    else if (d <= 80) launch_d<5, 3>(a, s);
+    else if (d <= 96) launch_d<6, 3>(a, s);
+    else if (d <= 128) launch_d<8, 4>(a, s);
+    else launch_d<10, 5>(a, s);
     return hipGetLastError();
 }
 

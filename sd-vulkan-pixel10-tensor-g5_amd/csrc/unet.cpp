@@ -665,7 +665,7 @@ int unet_profile(Ctx& c, int B, int H, int W, int L) {
         ms /= (float)r.reps;
         hipEventDestroy(r.e0);
         hipEventDestroy(r.e1);
-        if (dump) fprintf(dump, "%s,%s,%s,%.0f,%.0f,%.5f\n", r.cat.c_str(), r.kern.c_str(), r.shape.c_str(),
+        if (dump) fprintf(dump, "%s,\"%s\",\"%s\",%.0f,%.0f,%.5f\n", r.cat.c_str(), r.kern.c_str(), r.shape.c_str(),
                           r.flops, r.bytes, ms);
         for (const std::string& key : {r.cat, std::string("k:") + r.kern}) {
             ProfAcc& a = c.prof[key];
