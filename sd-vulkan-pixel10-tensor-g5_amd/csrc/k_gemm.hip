@@ -72,7 +72,7 @@ __device__ __forceinline__ int lds_swizzle(int row) {
     return BKT == 64 ? ((row >> 1) & 7) : ((row >> 2) & 3);
 }
 
-template <int MT, int NT, int WM, int WN, int BKT, int NS>
+template <int MT, int NT, int WM, int WN, int BKT, int NS, int AM>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
     constexpr int NW = WM * WN, NTH = NW * 64;
     constexpr int TMW = MT / WM, TNW = NT / WN;  // wave tile
@@ -111,77 +111,110 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
     // DMA lane assignment: instruction i of wave w fills tile rows
     // [(i*NW + w)*RPI, +RPI); lane l lands in row +(l / CPR), physical chunk l % CPR,
     // which holds logical chunk (l % CPR) ^ swizzle(row).
+    //
+    // Each lane's source for K tile k0 is precomputed up to an offset that the K loop
+    // adds (row pointer + k0 for dense A and for W; pixel offset + tap offset + channel
+    // for the implicit conv), so a K tile costs a few VALU per DMA instruction.  Rows
+    // past M / N repeat the last row: their results are never stored.  Out-of-range
+    // sources (conv padding, the K tail) read a zero page instead, chosen with selects
+    // (exactly AI + BI DMA instructions per thread and K tile, which the vmcnt waits
+    // below count on).
     const int lr = lane / CPR, pchunk = lane % CPR;
-    int a_m[AI], a_c[AI], a_b[AI], a_oy[AI], a_ox[AI];
-#pragma unroll
-    for (int i = 0; i < AI; ++i) {
-        const int row = (i * NW + wave) * RPI + lr;
-        a_c[i] = pchunk ^ lds_swizzle<BKT>(row);
-        const int m = min(m0 + row, a.M - 1);  // rows past M compute garbage that is never stored
-        a_m[i] = m;
-        if (a.amode == A_CONV3) {
-            const int hw = a.Ho * a.Wo;
-            a_b[i] = m / hw;
-            const int p = m - a_b[i] * hw;
-            a_oy[i] = p / a.Wo;
-            a_ox[i] = p - a_oy[i] * a.Wo;
-        } else {
-            a_b[i] = a_oy[i] = a_ox[i] = 0;
-        }
-    }
-    int b_n[BI], b_c[BI];
+    const f16* zero = (const f16*)g_zero_page;
+    const f16* pb[BI];
+    int b_c[BI];
 #pragma unroll
     for (int i = 0; i < BI; ++i) {
         const int row = (i * NW + wave) * RPI + lr;
-        b_c[i] = pchunk ^ lds_swizzle<BKT>(row);
-        b_n[i] = min(n0 + row, a.N - 1);
+        b_c[i] = (pchunk ^ lds_swizzle<BKT>(row)) * 8;
+        pb[i] = a.Wt + (int64_t)min(n0 + row, a.N - 1) * a.K + b_c[i];
     }
-    const bool tap_uniform = (a.amode == A_CONV3) && (a.Cin % BKT == 0);
-    const void* zero = (const void*)g_zero_page;
+    int a_c[AI];          // element offset of the lane's chunk within the K tile
+    const f16* pa[AI];    // dense: A row pointer (+chunk)
+    const f16* pa2[AI];   // dense, second source: A2 row pointer (+chunk - K1)
+    int a_off[AI];        // conv: offset of tap (0,0) of the lane's output pixel (+chunk)
+    int a_vm[AI];         // conv: bit ky*3+kx set when that tap is inside the image
+    int a_b[AI], a_oy[AI], a_ox[AI];  // conv geometry for the general (per-lane tap) path
+#pragma unroll
+    for (int i = 0; i < AI; ++i) {
+        const int row = (i * NW + wave) * RPI + lr;
+        a_c[i] = (pchunk ^ lds_swizzle<BKT>(row)) * 8;
+        const int m = min(m0 + row, a.M - 1);
+        if (AM == A_DENSE) {
+            pa[i] = a.A + (int64_t)m * a.lda + a_c[i];
+            pa2[i] = a.A2 ? a.A2 + (int64_t)m * a.lda2 + a_c[i] - a.K1 : pa[i];
+        } else {
+            const int hw = a.Ho * a.Wo;
+            const int bb = m / hw, p = m - bb * hw;
+            const int oy = p / a.Wo, ox = p - oy * a.Wo;
+            a_b[i] = bb; a_oy[i] = oy; a_ox[i] = ox;
+            const int y0 = oy * a.stride - 1, x0 = ox * a.stride - 1;
+            a_off[i] = ((bb * a.Hin + y0) * a.Win + x0) * a.Cin + a_c[i];
+            int vm = 0;
+#pragma unroll
+            for (int ky = 0; ky < 3; ++ky)
+#pragma unroll
+                for (int kx = 0; kx < 3; ++kx) {
+                    const int uy = (a.upsample ? oy - 1 : y0) + ky, ux = (a.upsample ? ox - 1 : x0) + kx;
+                    const int hl = a.upsample ? 2 * a.Hin : a.Hin, wl = a.upsample ? 2 * a.Win : a.Win;
+                    if (uy >= 0 && uy < hl && ux >= 0 && ux < wl) vm |= 1 << (ky * 3 + kx);
+                }
+            a_vm[i] = vm;
+        }
+    }
+    // conv fast path: each K tile lies inside one tap (Cin % BKT == 0) and the input
+    // is not upsampled, so the tap offset is one scalar per tile
+    const bool conv_fast = AM == A_CONV3 && a.Cin % BKT == 0 && !a.upsample;
+    int tap_next = 0, c_next = 0;  // tap / channel of the next tile issued (fast path)
+    if (conv_fast) { tap_next = kbeg / a.Cin; c_next = kbeg - tap_next * a.Cin; }
 
-    // Source address of each lane's 16-byte chunk, chosen with selects (no
-    // divergent branches around the DMA: exactly AI + BI DMA instructions per
-    // thread and K tile, which the vmcnt waits below count on).
+    auto dma = [&](const f16* src, f16* dst) __attribute__((always_inline)) {
+        __builtin_amdgcn_global_load_lds((const void*)src, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+    };
     auto issue = [&](int kt, int stage) __attribute__((always_inline)) {
         const int k0 = kbeg + kt * BKT;
+        const bool tail = k0 + BKT > kend;  // partial K tile: per-lane bound check
         f16* sA = smem + stage * STAGE;
         f16* sB = sA + MT * BKT;
-        if (a.amode == A_DENSE) {
+        if (AM == A_DENSE) {
+            const bool mixed = a.A2 && k0 < a.K1 && k0 + BKT > a.K1;  // tile straddles the split
+            const bool second = a.A2 && k0 >= a.K1;
 #pragma unroll
             for (int i = 0; i < AI; ++i) {
-                const int k = k0 + a_c[i] * 8;
-                const bool second = k >= a.K1;
-                const f16* base = second ? a.A2 : a.A;
-                const int64_t off = second ? (int64_t)a_m[i] * a.lda2 + (k - a.K1) : (int64_t)a_m[i] * a.lda + k;
-                const void* src = (k < kend) ? (const void*)(base + off) : zero;
-                __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(sA + (i * NW + wave) * RPI * BKT),
-                                                 16, 0, 0);
+                const f16* src = (mixed ? (k0 + a_c[i] >= a.K1) : second) ? pa2[i] : pa[i];
+                src += k0;
+                if (tail && k0 + a_c[i] >= kend) src = zero;
+                dma(src, sA + (i * NW + wave) * RPI * BKT);
+            }
+        } else if (conv_fast) {
+            const int tap = tap_next, ky = tap / 3, kx = tap - ky * 3;
+            const int toff = (ky * a.Win + kx) * a.Cin + c_next;
+            c_next += BKT;
+            if (c_next == a.Cin) { c_next = 0; ++tap_next; }
+#pragma unroll
+            for (int i = 0; i < AI; ++i) {
+                const bool ok = ((a_vm[i] >> tap) & 1) && !(tail && k0 + a_c[i] >= kend);
+                const f16* src = ok ? a.A + (uint32_t)(a_off[i] + toff) : zero;
+                dma(src, sA + (i * NW + wave) * RPI * BKT);
             }
         } else {
-            int tap_u = 0, c_u = 0;
-            if (tap_uniform) { tap_u = k0 / a.Cin; c_u = k0 - tap_u * a.Cin; }
 #pragma unroll
             for (int i = 0; i < AI; ++i) {
-                const int k = k0 + a_c[i] * 8;
-                const int tap = tap_uniform ? tap_u : k / a.Cin;
-                const int c = tap_uniform ? c_u + a_c[i] * 8 : k - tap * a.Cin;
+                const int k = k0 + a_c[i];
+                const int tap = k / a.Cin, c = k - tap * a.Cin;
                 const int ky = tap / 3, kx = tap - ky * 3;
                 const int uy = a_oy[i] * a.stride + ky - 1, ux = a_ox[i] * a.stride + kx - 1;
-                const int hlim = a.upsample ? 2 * a.Hin : a.Hin, wlim = a.upsample ? 2 * a.Win : a.Win;
-                const bool ok = (k < kend) & (uy >= 0) & (uy < hlim) & (ux >= 0) & (ux < wlim);
+                const bool ok = (k < kend) && ((a_vm[i] >> tap) & 1);
                 const int iy = a.upsample ? (uy >> 1) : uy, ix = a.upsample ? (ux >> 1) : ux;
                 const int64_t off = (((int64_t)a_b[i] * a.Hin + iy) * a.Win + ix) * a.Cin + c;
-                const void* src = ok ? (const void*)(a.A + off) : zero;
-                __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(sA + (i * NW + wave) * RPI * BKT),
-                                                 16, 0, 0);
+                dma(ok ? a.A + off : zero, sA + (i * NW + wave) * RPI * BKT);
             }
         }
 #pragma unroll
         for (int i = 0; i < BI; ++i) {
-            const int k = k0 + b_c[i] * 8;
-            const void* src = (k < kend) ? (const void*)(a.Wt + (int64_t)b_n[i] * a.K + k) : zero;
-            __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(sB + (i * NW + wave) * RPI * BKT),
-                                             16, 0, 0);
+            const f16* src = pb[i] + k0;
+            if (tail && k0 + b_c[i] >= kend) src = zero;
+            dma(src, sB + (i * NW + wave) * RPI * BKT);
         }
     };
 
@@ -497,6 +530,14 @@ size_t gemm_workspace_bytes(const GemmArgs& a) {
     return splits > 1 ? (size_t)splits * a.M * a.N * sizeof(float) : 0;
 }
 
+template <int AM>
+static void launch_cfg(int ci, dim3 grid, const GemmArgs& a, hipStream_t s) {
+    if (ci == 0) hipLaunchKernelGGL((gemm_kernel<256, 128, 4, 2, 64, 2, AM>), grid, dim3(512), 0, s, a);
+    else if (ci == 1) hipLaunchKernelGGL((gemm_kernel<128, 128, 2, 2, 32, 4, AM>), grid, dim3(256), 0, s, a);
+    else if (ci == 2) hipLaunchKernelGGL((gemm_kernel<128, 64, 2, 2, 32, 4, AM>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((gemm_kernel<128, 128, 2, 2, 64, 2, AM>), grid, dim3(256), 0, s, a);
+}
+
 hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s) {
     int ci, splits, kps;
     plan(a, ci, splits, kps);
@@ -519,10 +560,8 @@ hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s) {
     static const char* kNames[4] = {"gemm_kernel<256,128,4,2,64,2>", "gemm_kernel<128,128,2,2,32,4>",
                                     "gemm_kernel<128,64,2,2,32,4>", "gemm_kernel<128,128,2,2,64,2>"};
     launch_timed(kNames[ci], flops, k_bytes, [&] {
-        if (ci == 0) hipLaunchKernelGGL((gemm_kernel<256, 128, 4, 2, 64, 2>), grid, dim3(512), 0, s, a);
-        else if (ci == 1) hipLaunchKernelGGL((gemm_kernel<128, 128, 2, 2, 32, 4>), grid, dim3(256), 0, s, a);
-        else if (ci == 2) hipLaunchKernelGGL((gemm_kernel<128, 64, 2, 2, 32, 4>), grid, dim3(256), 0, s, a);
-        else hipLaunchKernelGGL((gemm_kernel<128, 128, 2, 2, 64, 2>), grid, dim3(256), 0, s, a);
+        if (a.amode == A_DENSE) launch_cfg<A_DENSE>(ci, grid, a, s);
+        else launch_cfg<A_CONV3>(ci, grid, a, s);
     });
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || splits == 1) return e;
