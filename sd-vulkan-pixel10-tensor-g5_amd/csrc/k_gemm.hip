@@ -112,37 +112,45 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
     // [(i*NW + w)*RPI, +RPI); lane l lands in row +(l / CPR), physical chunk l % CPR,
     // which holds logical chunk (l % CPR) ^ swizzle(row).
     //
-    // Each lane's source for K tile k0 is precomputed up to an offset that the K loop
-    // adds (row pointer + k0 for dense A and for W; pixel offset + tap offset + channel
-    // for the implicit conv), so a K tile costs a few VALU per DMA instruction.  Rows
-    // past M / N repeat the last row: their results are never stored.  Out-of-range
-    // sources (conv padding, the K tail) read a zero page instead, chosen with selects
-    // (exactly AI + BI DMA instructions per thread and K tile, which the vmcnt waits
-    // below count on).
+    // Steady-state K tiles load through buffer_load ... lds: the operand base is a
+    // wave-uniform buffer resource, each lane's byte offset is precomputed once (row
+    // offset + chunk), and the K position is the scalar soffset, so a dense or weight
+    // DMA costs no VALU.  Implicit-conv rows add a scalar tap offset and select
+    // 0x80000000 for taps outside the image: an offset past the resource's range reads
+    // zeros.  Rows past M / N repeat the last row (results never stored).  K tails,
+    // tiles straddling the dense two-source split, and the conv cases whose tap
+    // changes within a tile (Cin % BK != 0, upsampled input) take a per-lane pointer
+    // path with global_load_lds and a zero page.  Every path issues exactly AI + BI
+    // DMA instructions per thread and K tile, which the vmcnt waits below count on.
     const int lr = lane / CPR, pchunk = lane % CPR;
     const f16* zero = (const f16*)g_zero_page;
-    const f16* pb[BI];
+    constexpr uint32_t kOOB = 0x80000000u;
+    const __amdgpu_buffer_rsrc_t rsB =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.Wt, (short)0, a.N * a.K * 2, 0x00020000);
+    uint32_t voB[BI];
     int b_c[BI];
 #pragma unroll
     for (int i = 0; i < BI; ++i) {
         const int row = (i * NW + wave) * RPI + lr;
         b_c[i] = (pchunk ^ lds_swizzle<BKT>(row)) * 8;
-        pb[i] = a.Wt + (int64_t)min(n0 + row, a.N - 1) * a.K + b_c[i];
+        voB[i] = (uint32_t)((min(n0 + row, a.N - 1) * a.K + b_c[i]) * 2);
     }
     int a_c[AI];          // element offset of the lane's chunk within the K tile
-    const f16* pa[AI];    // dense: A row pointer (+chunk)
-    const f16* pa2[AI];   // dense, second source: A2 row pointer (+chunk - K1)
-    int a_off[AI];        // conv: offset of tap (0,0) of the lane's output pixel (+chunk)
+    int a_m[AI];          // dense: row (clamped)
+    uint32_t voA[AI];     // dense: byte offset of (row, chunk) in A
+    uint32_t voA2[AI];    // dense: byte offset of (row, chunk) in A2
+    int a_off[AI];        // conv: element offset of tap (0,0) of the lane's output pixel (+chunk)
     int a_vm[AI];         // conv: bit ky*3+kx set when that tap is inside the image
-    int a_b[AI], a_oy[AI], a_ox[AI];  // conv geometry for the general (per-lane tap) path
+    int a_b[AI], a_oy[AI], a_ox[AI];  // conv geometry for the per-lane path
 #pragma unroll
     for (int i = 0; i < AI; ++i) {
         const int row = (i * NW + wave) * RPI + lr;
         a_c[i] = (pchunk ^ lds_swizzle<BKT>(row)) * 8;
         const int m = min(m0 + row, a.M - 1);
+        a_m[i] = m;
         if (AM == A_DENSE) {
-            pa[i] = a.A + (int64_t)m * a.lda + a_c[i];
-            pa2[i] = a.A2 ? a.A2 + (int64_t)m * a.lda2 + a_c[i] - a.K1 : pa[i];
+            voA[i] = (uint32_t)((m * a.lda + a_c[i]) * 2);
+            voA2[i] = a.A2 ? (uint32_t)((m * a.lda2 + a_c[i]) * 2) : 0u;
         } else {
             const int hw = a.Ho * a.Wo;
             const int bb = m / hw, p = m - bb * hw;
@@ -162,6 +170,11 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
             a_vm[i] = vm;
         }
     }
+    const __amdgpu_buffer_rsrc_t rsA = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)a.A, (short)0,
+        AM == A_DENSE ? a.M * a.lda * 2 : a.Bn * a.Hin * a.Win * a.Cin * 2, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsA2 = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(a.A2 ? a.A2 : a.A), (short)0, a.A2 ? a.M * a.lda2 * 2 : 0, 0x00020000);
     // conv fast path: each K tile lies inside one tap (Cin % BKT == 0) and the input
     // is not upsampled, so the tap offset is one scalar per tile
     const bool conv_fast = AM == A_CONV3 && a.Cin % BKT == 0 && !a.upsample;
@@ -171,20 +184,31 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
     auto dma = [&](const f16* src, f16* dst) __attribute__((always_inline)) {
         __builtin_amdgcn_global_load_lds((const void*)src, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
     };
+    auto bdma = [&](__amdgpu_buffer_rsrc_t rs, uint32_t vo, int so, f16* dst) __attribute__((always_inline)) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)dst, 16, vo, so, 0, 0);
+    };
     auto issue = [&](int kt, int stage) __attribute__((always_inline)) {
         const int k0 = kbeg + kt * BKT;
-        const bool tail = k0 + BKT > kend;  // partial K tile: per-lane bound check
+        const bool tail = k0 + BKT > kend;  // partial K tile
         f16* sA = smem + stage * STAGE;
         f16* sB = sA + MT * BKT;
         if (AM == A_DENSE) {
-            const bool mixed = a.A2 && k0 < a.K1 && k0 + BKT > a.K1;  // tile straddles the split
-            const bool second = a.A2 && k0 >= a.K1;
+            const bool in1 = !a.A2 || k0 + BKT <= a.K1, in2 = a.A2 && k0 >= a.K1;
+            if (!tail && in1) {
 #pragma unroll
-            for (int i = 0; i < AI; ++i) {
-                const f16* src = (mixed ? (k0 + a_c[i] >= a.K1) : second) ? pa2[i] : pa[i];
-                src += k0;
-                if (tail && k0 + a_c[i] >= kend) src = zero;
-                dma(src, sA + (i * NW + wave) * RPI * BKT);
+                for (int i = 0; i < AI; ++i) bdma(rsA, voA[i], k0 * 2, sA + (i * NW + wave) * RPI * BKT);
+            } else if (!tail && in2) {
+#pragma unroll
+                for (int i = 0; i < AI; ++i)
+                    bdma(rsA2, voA2[i], (k0 - a.K1) * 2, sA + (i * NW + wave) * RPI * BKT);
+            } else {
+#pragma unroll
+                for (int i = 0; i < AI; ++i) {
+                    const int k = k0 + a_c[i];
+                    const f16* src = (a.A2 && k >= a.K1) ? a.A2 + (int64_t)a_m[i] * a.lda2 + (k - a.K1)
+                                                         : a.A + (int64_t)a_m[i] * a.lda + k;
+                    dma(k < kend ? src : zero, sA + (i * NW + wave) * RPI * BKT);
+                }
             }
         } else if (conv_fast) {
             const int tap = tap_next, ky = tap / 3, kx = tap - ky * 3;
@@ -194,8 +218,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
 #pragma unroll
             for (int i = 0; i < AI; ++i) {
                 const bool ok = ((a_vm[i] >> tap) & 1) && !(tail && k0 + a_c[i] >= kend);
-                const f16* src = ok ? a.A + (uint32_t)(a_off[i] + toff) : zero;
-                dma(src, sA + (i * NW + wave) * RPI * BKT);
+                bdma(rsA, ok ? (uint32_t)((a_off[i] + toff) * 2) : kOOB, 0, sA + (i * NW + wave) * RPI * BKT);
             }
         } else {
 #pragma unroll
@@ -210,11 +233,13 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
                 dma(ok ? a.A + off : zero, sA + (i * NW + wave) * RPI * BKT);
             }
         }
+        if (!tail) {
 #pragma unroll
-        for (int i = 0; i < BI; ++i) {
-            const f16* src = pb[i] + k0;
-            if (tail && k0 + b_c[i] >= kend) src = zero;
-            dma(src, sB + (i * NW + wave) * RPI * BKT);
+            for (int i = 0; i < BI; ++i) bdma(rsB, voB[i], k0 * 2, sB + (i * NW + wave) * RPI * BKT);
+        } else {
+#pragma unroll
+            for (int i = 0; i < BI; ++i)
+                bdma(rsB, k0 + b_c[i] < kend ? voB[i] + k0 * 2 : kOOB, 0, sB + (i * NW + wave) * RPI * BKT);
         }
     };
 
@@ -546,6 +571,12 @@ hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s) {
     a.k_per_split = kps;
     a.partial = splits > 1 ? ws : nullptr;
     if (splits > 1 && ws == nullptr) return hipErrorInvalidValue;
+    // operands are addressed with 32-bit byte offsets (buffer resources)
+    const int64_t lim = 0x7fffffff;
+    if (2 * (int64_t)a.N * a.K > lim) return hipErrorInvalidValue;
+    if (a.amode == A_DENSE && (2 * (int64_t)a.M * a.lda > lim || (a.A2 && 2 * (int64_t)a.M * a.lda2 > lim)))
+        return hipErrorInvalidValue;
+    if (a.amode == A_CONV3 && 2 * (int64_t)a.Bn * a.Hin * a.Win * a.Cin > lim) return hipErrorInvalidValue;
     const Cfg& g = kCfgs[ci];
     dim3 grid(ceil_div(a.M, g.mt) * ceil_div(a.N, g.nt), 1, splits);
     // algorithmic traffic: A once (the conv source image, not its im2col), W once, output
