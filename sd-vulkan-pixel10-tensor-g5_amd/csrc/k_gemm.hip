@@ -494,37 +494,32 @@ __global__ void splitk_reduce_kernel(GemmArgs a) {
 
 namespace {
 struct Cfg {
-    int mt, nt, per_cu;  // tile, resident blocks per CU (LDS-limited)
-    double eff;          // relative per-FLOP throughput of the tile shape
+    int mt, nt, per_cu;   // tile, resident blocks per CU (LDS-limited)
+    double rate1, rate2;  // measured MFMA FLOP/s of one CU running 1 / 2 such blocks
+    double t_fix;         // per-block prologue + epilogue time
     const char* name;
 };
-// 0: 256x128, 8 waves of 64x64, BK 64, 2-stage ring (96 KB LDS, one block per CU)
-// 1: 128x128, 4 waves of 64x64, BK 32, 4-stage ring (64 KB, two per CU)
-// 2: 128x64,  4 waves of 64x32, BK 32, 4-stage ring (48 KB, three per CU)
-// 3: 128x128, 4 waves of 64x64, BK 64, 2-stage ring (64 KB, two per CU)
-const Cfg kCfgs[4] = {{256, 128, 1, 1.0, "gemm_256x128"},
-                      {128, 128, 2, 0.95, "gemm_128x128"},
-                      {128, 64, 3, 0.75, "gemm_128x64"},
-                      {128, 128, 2, 0.95, "gemm_128x128k64"}};
+// 0: 256x128, 8 waves of 64x64, BK 64, 2-stage ring (96 KB: one block per CU)
+// 1: 128x128, 4 waves of 64x64, BK 64, 2-stage ring (64 KB: two per CU)
+// 2: 128x64,  4 waves of 64x32, BK 64, 3-stage ring (72 KB: two per CU)
+const Cfg kCfgs[3] = {{256, 128, 1, 3.3e12, 3.3e12, 4.5e-6, "gemm_kernel<256,128,4,2,64,2>"},
+                      {128, 128, 2, 2.4e12, 3.4e12, 3.0e-6, "gemm_kernel<128,128,2,2,64,2>"},
+                      {128, 64, 2, 1.6e12, 2.4e12, 2.5e-6, "gemm_kernel<128,64,2,2,64,3>"}};
 
 int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
-// Pick the tile shape and split-K factor with the lowest modelled time.  A block
-// that has its CU to itself runs at the full per-CU rate; blocks sharing a CU
-// split it.  Each block also pays a fixed prologue / epilogue cost, and a split
-// K pays the fp32 partial round trip plus the reduce launch.
+// Pick the tile shape and split-K factor with the lowest modelled time.  Blocks are
+// spread evenly over the 256 CUs; the busiest CU runs its blocks two at a time where
+// the tile allows two per CU (a lone block cannot keep a CU busy: rate1 < rate2),
+// each round paying a fixed prologue / epilogue cost.  A split K adds the fp32
+// partial round trip (mostly L2 / Infinity Cache resident) and the reduce launch.
 void plan(const GemmArgs& a, int& ci, int& splits, int& kps) {
-    const double cu_rate = 2.5e12;  // sustained MFMA FLOP/s per CU for these tiles
-    const double t_block = 2.0e-6;  // per-block fixed cost
     const int nkt = ceil_div(a.K, 64);
     double best = 1e30;
     ci = 1; splits = 1; kps = nkt * 64;
-    for (int c = 0; c < 4; ++c) {
+    for (int c = 0; c < 3; ++c) {
         const Cfg& g = kCfgs[c];
         if (a.geglu && g.nt < 128) continue;  // GEGLU pairs 32-column blocks within a 64-wide wave tile
-        // the implicit-GEMM conv gathers are cheaper per FLOP with 64-wide K tiles
-        if (a.amode == A_CONV3 && c == 1) continue;
-        if (a.amode != A_CONV3 && c == 3) continue;
         const int tiles = ceil_div(a.M, g.mt) * ceil_div(a.N, g.nt);
         static const int cand[] = {1, 2, 3, 4, 6, 8, 12, 16, 24, 32};
         for (int s : cand) {
@@ -532,11 +527,11 @@ void plan(const GemmArgs& a, int& ci, int& splits, int& kps) {
             const int kt_per = ceil_div(nkt, s);
             const int se = ceil_div(nkt, kt_per);
             const long blocks = (long)tiles * se;
-            const int conc = (int)std::min<long>(g.per_cu, (blocks + 255) / 256);
-            const long rounds = (blocks + 256L * conc - 1) / (256L * conc);
-            const double work = 2.0 * g.mt * g.nt * kt_per * 64.0;
-            double t = rounds * (work * conc / (g.eff * cu_rate) + t_block);
-            if (se > 1) t += (double)se * a.M * a.N * 8.0 / 4.0e12 + 2.5e-6;
+            const long load = (blocks + 255) / 256;  // blocks on the busiest CU
+            const double w = 2.0 * g.mt * g.nt * kt_per * 64.0;
+            const long pairs = g.per_cu >= 2 ? load / 2 : 0, singles = load - 2 * pairs;
+            double t = pairs * (2.0 * w / g.rate2 + g.t_fix) + singles * (w / g.rate1 + g.t_fix);
+            if (se > 1) t += (double)se * a.M * a.N * 8.0 / 20.0e12 + 4.0e-6;
             if (t < best * 0.98) { best = t; ci = c; splits = se; kps = kt_per * 64; }
         }
     }
@@ -558,9 +553,8 @@ size_t gemm_workspace_bytes(const GemmArgs& a) {
 template <int AM>
 static void launch_cfg(int ci, dim3 grid, const GemmArgs& a, hipStream_t s) {
     if (ci == 0) hipLaunchKernelGGL((gemm_kernel<256, 128, 4, 2, 64, 2, AM>), grid, dim3(512), 0, s, a);
-    else if (ci == 1) hipLaunchKernelGGL((gemm_kernel<128, 128, 2, 2, 32, 4, AM>), grid, dim3(256), 0, s, a);
-    else if (ci == 2) hipLaunchKernelGGL((gemm_kernel<128, 64, 2, 2, 32, 4, AM>), grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((gemm_kernel<128, 128, 2, 2, 64, 2, AM>), grid, dim3(256), 0, s, a);
+    else if (ci == 1) hipLaunchKernelGGL((gemm_kernel<128, 128, 2, 2, 64, 2, AM>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((gemm_kernel<128, 64, 2, 2, 64, 3, AM>), grid, dim3(256), 0, s, a);
 }
 
 hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s) {
@@ -588,9 +582,7 @@ hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s) {
     const double part_bytes = splits > 1 ? 4.0 * splits * a.M * a.N : 0.0;
     const double flops = 2.0 * a.M * a.N * a.K;
     const double k_bytes = a_bytes + 2.0 * a.N * a.K + (splits > 1 ? part_bytes : out_bytes);
-    static const char* kNames[4] = {"gemm_kernel<256,128,4,2,64,2>", "gemm_kernel<128,128,2,2,32,4>",
-                                    "gemm_kernel<128,64,2,2,32,4>", "gemm_kernel<128,128,2,2,64,2>"};
-    launch_timed(kNames[ci], flops, k_bytes, [&] {
+    launch_timed(kCfgs[ci].name, flops, k_bytes, [&] {
         if (a.amode == A_DENSE) launch_cfg<A_DENSE>(ci, grid, a, s);
         else launch_cfg<A_CONV3>(ci, grid, a, s);
     });
