@@ -60,6 +60,78 @@ __device__ __forceinline__ void wait_vmcnt_lgkm0() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0x0 << 8) | ((N >> 4) << 14));
 }
 
+// Sum split-K partials and apply the epilogue.  Vector path: 8 output columns
+// (N % 8 == 0 and not NCHW); scalar path: one element.
+__device__ __forceinline__ void reduce_scalar(const GemmArgs& a, int m, int nout) {
+    const int64_t mn = (int64_t)a.M * a.N;
+    const int n = a.geglu ? (nout >> 5) * 64 + (nout & 31) : nout;
+    float v = 0.f, g = 0.f;
+    for (int z = 0; z < a.splits; ++z) {
+        v += a.partial[z * mn + (int64_t)m * a.N + n];
+        if (a.geglu) g += a.partial[z * mn + (int64_t)m * a.N + n + 32];
+    }
+    epi_store(a, m, n, v, g, nout);
+}
+
+__device__ __forceinline__ void reduce_vec8(const GemmArgs& a, int m, int nout) {
+    const int64_t mn = (int64_t)a.M * a.N;
+    const int n = a.geglu ? (nout >> 5) * 64 + (nout & 31) : nout;
+    float v[8], g[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) { v[e] = 0.f; g[e] = 0.f; }
+    for (int z = 0; z < a.splits; ++z) {
+        const float* p = a.partial + z * mn + (int64_t)m * a.N + n;
+        const float4 p0 = *(const float4*)p, p1 = *(const float4*)(p + 4);
+        v[0] += p0.x; v[1] += p0.y; v[2] += p0.z; v[3] += p0.w;
+        v[4] += p1.x; v[5] += p1.y; v[6] += p1.z; v[7] += p1.w;
+        if (a.geglu) {
+            const float4 q0 = *(const float4*)(p + 32), q1 = *(const float4*)(p + 36);
+            g[0] += q0.x; g[1] += q0.y; g[2] += q0.z; g[3] += q0.w;
+            g[4] += q1.x; g[5] += q1.y; g[6] += q1.z; g[7] += q1.w;
+        }
+    }
+    uint4 rr = make_uint4(0, 0, 0, 0);
+    if (a.res) rr = *(const uint4*)(a.res + (int64_t)m * a.ldr + nout);
+    const f16* rh = (const f16*)&rr;
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        float x = v[e], gt = g[e];
+        if (a.bias) { x += (float)a.bias[n + e]; if (a.geglu) gt += (float)a.bias[n + 32 + e]; }
+        if (a.bias2) { x += a.bias2[n + e]; if (a.geglu) gt += a.bias2[n + 32 + e]; }
+        if (a.geglu) x *= gelu_erf(gt);
+        if (a.res) x += (float)rh[e];
+        o[e] = x;
+    }
+    if (a.out_mode == OUT_F16) {
+        uint4 ov;
+        f16* oh = (f16*)&ov;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) oh[e] = (f16)o[e];
+        *(uint4*)((f16*)a.C + (int64_t)m * a.ldc + nout) = ov;
+    } else {
+        float* cp = (float*)a.C + (int64_t)m * a.ldc + nout;
+        *(float4*)cp = make_float4(o[0], o[1], o[2], o[3]);
+        *(float4*)(cp + 4) = make_float4(o[4], o[5], o[6], o[7]);
+    }
+}
+
+__global__ void splitk_reduce_kernel(GemmArgs a) {
+    const int nout_cols = a.geglu ? a.N / 2 : a.N;
+    const bool vec = a.out_mode != OUT_F32_NCHW && (a.N & 7) == 0;
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (!vec) {
+        if (idx >= (int64_t)a.M * nout_cols) return;
+        const int m = (int)(idx / nout_cols);
+        reduce_scalar(a, m, (int)(idx - (int64_t)m * nout_cols));
+        return;
+    }
+    const int cpr = nout_cols / 8;
+    if (idx >= (int64_t)a.M * cpr) return;
+    const int m = (int)(idx / cpr);
+    reduce_vec8(a, m, (int)(idx - (int64_t)m * cpr) * 8);
+}
+
 // Main loop: NS-stage LDS ring fed by global_load_lds_dwordx4 (direct to LDS, no
 // register staging), NS-1 K tiles in flight while one is consumed, one s_barrier
 // per K tile.  LDS rows are BK halves (64 or 128 bytes) with the 16-byte chunk
@@ -424,73 +496,6 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
         }
     }
 }
-
-// Sum split-K partials and apply the epilogue.  Vector path: one thread per 8
-// output columns (N % 8 == 0 and not NCHW); otherwise one thread per element.
-__global__ void splitk_reduce_kernel(GemmArgs a) {
-    const int nout_cols = a.geglu ? a.N / 2 : a.N;
-    const int64_t mn = (int64_t)a.M * a.N;
-    const bool vec = a.out_mode != OUT_F32_NCHW && (a.N & 7) == 0;
-    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (!vec) {
-        if (idx >= (int64_t)a.M * nout_cols) return;
-        const int m = (int)(idx / nout_cols);
-        const int nout = (int)(idx - (int64_t)m * nout_cols);
-        const int n = a.geglu ? (nout >> 5) * 64 + (nout & 31) : nout;
-        float v = 0.f, g = 0.f;
-        for (int z = 0; z < a.splits; ++z) {
-            v += a.partial[z * mn + (int64_t)m * a.N + n];
-            if (a.geglu) g += a.partial[z * mn + (int64_t)m * a.N + n + 32];
-        }
-        epi_store(a, m, n, v, g, nout);
-        return;
-    }
-    const int cpr = nout_cols / 8;
-    if (idx >= (int64_t)a.M * cpr) return;
-    const int m = (int)(idx / cpr);
-    const int nout = (int)(idx - (int64_t)m * cpr) * 8;
-    const int n = a.geglu ? (nout >> 5) * 64 + (nout & 31) : nout;
-    float v[8], g[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) { v[e] = 0.f; g[e] = 0.f; }
-    for (int z = 0; z < a.splits; ++z) {
-        const float* p = a.partial + z * mn + (int64_t)m * a.N + n;
-        const float4 p0 = *(const float4*)p, p1 = *(const float4*)(p + 4);
-        v[0] += p0.x; v[1] += p0.y; v[2] += p0.z; v[3] += p0.w;
-        v[4] += p1.x; v[5] += p1.y; v[6] += p1.z; v[7] += p1.w;
-        if (a.geglu) {
-            const float4 q0 = *(const float4*)(p + 32), q1 = *(const float4*)(p + 36);
-            g[0] += q0.x; g[1] += q0.y; g[2] += q0.z; g[3] += q0.w;
-            g[4] += q1.x; g[5] += q1.y; g[6] += q1.z; g[7] += q1.w;
-        }
-    }
-    uint4 rr = make_uint4(0, 0, 0, 0);
-    if (a.res) rr = *(const uint4*)(a.res + (int64_t)m * a.ldr + nout);
-    const f16* rh = (const f16*)&rr;
-    float o[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        float x = v[e], gt = g[e];
-        if (a.bias) { x += (float)a.bias[n + e]; if (a.geglu) gt += (float)a.bias[n + 32 + e]; }
-        if (a.bias2) { x += a.bias2[n + e]; if (a.geglu) gt += a.bias2[n + 32 + e]; }
-        if (a.geglu) x *= gelu_erf(gt);
-        if (a.res) x += (float)rh[e];
-        o[e] = x;
-    }
-    if (a.out_mode == OUT_F16) {
-        uint4 ov;
-        f16* oh = (f16*)&ov;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) oh[e] = (f16)o[e];
-        *(uint4*)((f16*)a.C + (int64_t)m * a.ldc + nout) = ov;
-    } else {
-        float* cp = (float*)a.C + (int64_t)m * a.ldc + nout;
-        *(float4*)cp = make_float4(o[0], o[1], o[2], o[3]);
-        *(float4*)(cp + 4) = make_float4(o[4], o[5], o[6], o[7]);
-    }
-}
-
-// ----------------------------------------------------------------- dispatch
 
 namespace {
 struct Cfg {

@@ -89,6 +89,7 @@ def test_layernorm(op_engine, T, C):
     (8192, 320, 1280, 0, True, True, False, False),   # FF out
     (154, 2560, 768, 0, False, False, False, False),  # cross K/V (B=2 x 77 tokens)
     (128, 1280, 5120, 0, True, True, False, False),   # split-K (mid FF out)
+    (128, 2560, 1280, 0, True, False, True, False),   # split-K with GEGLU (mid FF proj)
     (512, 1280, 2560, 1280, True, False, False, False),  # 1x1 shortcut over a concat
     (77, 64, 64, 0, True, False, False, True),        # ragged M, N <= 64 tile, fp32 out
     (100, 128, 128, 0, True, False, True, False),     # GEGLU with ragged M
