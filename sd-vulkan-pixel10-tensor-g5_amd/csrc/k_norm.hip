@@ -13,6 +13,11 @@
 //     optional SiLU, 16-byte loads and stores.
 // Both passes accept a second source concatenated along channels (the up-path
 // skip concat, vk_engine.cpp:678-688), so the concat is never materialised.
+// When one (image, group) slab is small (HW * C/G <= 32K elements: the 32x32 and
+// smaller levels of the 64x64 UNet) and fits the registers of a 1024-thread block,
+// a single kernel does it all: the slab is loaded once, mean and variance are
+// reduced exactly in two passes over the registers, and the normalised values are
+// stored -- one launch, one read and one write of the tensor.
 //
 // LayerNorm replaces layernorm_f32.comp (vk_engine.cpp:652): one wave per token,
 // exact two-pass mean / variance in registers.
@@ -153,6 +158,105 @@ __global__ void zero_kernel(uint4* p, int64_t n16) {
     if (i < n16) p[i] = make_uint4(0, 0, 0, 0);
 }
 
+// ----------------------------------------------------------------- single-pass GroupNorm
+
+static constexpr int GNF_THREADS = 1024;
+
+// Sum over the block of one float per thread, in fp64 across waves; every thread
+// gets the result.
+__device__ __forceinline__ double gnf_block_sum(float v, double* red) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __syncthreads();  // red[] may still be read by the previous reduction
+    if (lane == 0) red[wave] = (double)v;
+    __syncthreads();
+    double t = 0.0;
+#pragma unroll
+    for (int w = 0; w < GNF_THREADS / 64; ++w) t += red[w];
+    return t;
+}
+
+// One block per (group, image).  Thread t owns channel pair t % (cpg/2) of the group
+// and pixels t / (cpg/2) + k*P (P = pixels per sweep of the block), k < EP: each
+// load / store is one 4-byte pair at a fixed stride, and pairs never straddle the
+// concat split (C1 and C/G are even).
+template <int EP>
+__global__ __launch_bounds__(GNF_THREADS) void gn_fused_kernel(const f16* x, const f16* x2, int C1, int C2,
+                                                               const f16* gamma, const f16* beta, f16* y,
+                                                               int B, int HW, int G, float eps, int silu) {
+    __shared__ double red[GNF_THREADS / 64];
+    const int C = C1 + C2, cpg = C / G, hpg = cpg / 2;
+    const int g = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+    const int P = GNF_THREADS / hpg;
+    const int cp = tid % hpg, pp0 = tid / hpg;
+    const bool act = pp0 < P;
+    const int pp = act ? pp0 : P - 1;
+    const int c = g * cpg + 2 * cp;
+    // All loads are issued before any is used, with 32-bit byte offsets into the
+    // source; pixels past HW reload pixel HW-1 and are not accumulated.
+    uint32_t raw[EP];
+    if (c < C1) {
+        const __amdgpu_buffer_rsrc_t rs =
+            __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, B * HW * C1 * 2, 0x00020000);
+        const int vo = ((int)b * HW * C1 + c) * 2;
+#pragma unroll
+        for (int k = 0; k < EP; ++k)
+            raw[k] = __builtin_amdgcn_raw_buffer_load_b32(rs, vo + min(pp + k * P, HW - 1) * C1 * 2, 0, 0);
+    } else {
+        const __amdgpu_buffer_rsrc_t rs =
+            __builtin_amdgcn_make_buffer_rsrc((void*)x2, (short)0, B * HW * C2 * 2, 0x00020000);
+        const int vo = ((int)b * HW * C2 + (c - C1)) * 2;
+#pragma unroll
+        for (int k = 0; k < EP; ++k)
+            raw[k] = __builtin_amdgcn_raw_buffer_load_b32(rs, vo + min(pp + k * P, HW - 1) * C2 * 2, 0, 0);
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < EP; ++k) {
+        if (act && pp + k * P < HW) {
+            const f16* h = (const f16*)&raw[k];
+            s += (float)h[0] + (float)h[1];
+        }
+    }
+    const double n = (double)HW * cpg;
+    const double mean = gnf_block_sum(s, red) / n;
+    const float mf = (float)mean;
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < EP; ++k) {
+        if (act && pp + k * P < HW) {
+            const f16* h = (const f16*)&raw[k];
+            const float d0 = (float)h[0] - mf, d1 = (float)h[1] - mf;
+            ss += d0 * d0 + d1 * d1;
+        }
+    }
+    const double var = gnf_block_sum(ss, red) / n;
+    const float rstd = (float)(1.0 / sqrt(var + (double)eps));
+    float sc[2], sh[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        sc[e] = rstd * (float)gamma[c + e];
+        sh[e] = (float)beta[c + e] - mf * sc[e];
+    }
+    f16* dst = y + c;
+#pragma unroll
+    for (int k = 0; k < EP; ++k) {
+        const int p = pp + k * P;
+        if (!act || p >= HW) continue;
+        const f16* h = (const f16*)&raw[k];
+        uint32_t o;
+        f16* oh = (f16*)&o;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            float z = (float)h[e] * sc[e] + sh[e];
+            if (silu) z = silu_f(z);
+            oh[e] = (f16)z;
+        }
+        *(uint32_t*)(dst + ((int64_t)b * HW + p) * C) = o;
+    }
+}
+
 hipError_t zero_launch(void* p, size_t bytes, hipStream_t s) {
     const int64_t n16 = (int64_t)((bytes + 15) / 16);
     if (n16 == 0) return hipSuccess;
@@ -167,8 +271,28 @@ hipError_t groupnorm_launch(const f16* x, const f16* x2, int C1, int C2, const f
                             double* acc, hipStream_t s) {
     const int C = C1 + C2;
     if (G > GN_MAXG || C > GN_MAXC || C % G || C % 8 || C1 % 8 || (C2 && !x2)) return hipErrorInvalidValue;
-    GnGeom g = gn_geom(HW, C);
     const double xbytes = 2.0 * B * HW * C;
+    const int cpg = C / G;
+    const int sweep = cpg % 2 == 0 ? GNF_THREADS / (cpg / 2) : 0;  // pixels per block sweep
+    const int nsweep = sweep ? (HW + sweep - 1) / sweep : 1 << 30;
+    // one block per (image, group) wins while the slab is small; larger slabs stream
+    // faster through the chunked two-kernel path, which spreads them over the chip
+    if (cpg % 2 == 0 && C1 % 2 == 0 && cpg / 2 <= GNF_THREADS && nsweep <= 32 &&
+        (int64_t)HW * cpg <= 32768 && 2 * (int64_t)B * HW * C < 0x7fffffff) {
+        const int ep = nsweep <= 4 ? 4 : nsweep <= 8 ? 8 : nsweep <= 16 ? 16 : 32;
+        static const char* kNames[4] = {"gn_fused_kernel<4>", "gn_fused_kernel<8>", "gn_fused_kernel<16>",
+                                        "gn_fused_kernel<32>"};
+        const int vi = ep == 4 ? 0 : ep == 8 ? 1 : ep == 16 ? 2 : 3;
+        const dim3 grid(G, B);
+        launch_timed(kNames[vi], 0.0, 2.0 * xbytes, [&] {
+            if (ep == 4) hipLaunchKernelGGL(gn_fused_kernel<4>, grid, dim3(GNF_THREADS), 0, s, x, x2, C1, C2, gamma, beta, y, B, HW, G, eps, silu);
+            else if (ep == 8) hipLaunchKernelGGL(gn_fused_kernel<8>, grid, dim3(GNF_THREADS), 0, s, x, x2, C1, C2, gamma, beta, y, B, HW, G, eps, silu);
+            else if (ep == 16) hipLaunchKernelGGL(gn_fused_kernel<16>, grid, dim3(GNF_THREADS), 0, s, x, x2, C1, C2, gamma, beta, y, B, HW, G, eps, silu);
+            else hipLaunchKernelGGL(gn_fused_kernel<32>, grid, dim3(GNF_THREADS), 0, s, x, x2, C1, C2, gamma, beta, y, B, HW, G, eps, silu);
+        });
+        return hipGetLastError();
+    }
+    GnGeom g = gn_geom(HW, C);
     launch_timed("gn_stats_kernel", 0.0, xbytes, [&] {
         hipLaunchKernelGGL(gn_stats_kernel, dim3(g.nchunk, B), dim3(GN_THREADS), 0, s, x, x2, C1, C2, HW,
                            g.P, G, acc);

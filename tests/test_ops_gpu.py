@@ -37,6 +37,8 @@ def t(a):
     (2, 32, 32, 640, 320, True),    # concat 960 @32^2
     (3, 7, 9, 64, 0, True),         # ragged pixel count
     (16, 8, 8, 2560, 0, False),     # C > 2048 (two channel windows per block)
+    (2, 64, 64, 640, 320, True),    # concat 960 @64^2: group slab too large for one block
+    (1, 5, 5, 96, 0, False),        # 3 channels per group (odd): two-pass path
 ])
 def test_groupnorm(op_engine, B, H, W, C1, C2, silu):
     say(f"groupnorm B={B} {H}x{W} C1={C1} C2={C2} silu={silu}")
