@@ -502,14 +502,17 @@ struct Cfg {
     int mt, nt, per_cu;   // tile, resident blocks per CU (LDS-limited)
     double rate1, rate2;  // measured MFMA FLOP/s of one CU running 1 / 2 such blocks
     double t_fix;         // per-block prologue + epilogue time
-    const char* name;
 };
 // 0: 256x128, 8 waves of 64x64, BK 64, 2-stage ring (96 KB: one block per CU)
 // 1: 128x128, 4 waves of 64x64, BK 64, 2-stage ring (64 KB: two per CU)
 // 2: 128x64,  4 waves of 64x32, BK 64, 3-stage ring (72 KB: two per CU)
-const Cfg kCfgs[3] = {{256, 128, 1, 3.3e12, 3.3e12, 4.5e-6, "gemm_kernel<256,128,4,2,64,2>"},
-                      {128, 128, 2, 2.4e12, 3.4e12, 3.0e-6, "gemm_kernel<128,128,2,2,64,2>"},
-                      {128, 64, 2, 1.6e12, 2.4e12, 2.5e-6, "gemm_kernel<128,64,2,2,64,3>"}};
+const Cfg kCfgs[3] = {{256, 128, 1, 3.3e12, 3.3e12, 4.5e-6},
+                      {128, 128, 2, 2.4e12, 3.4e12, 3.0e-6},
+                      {128, 64, 2, 1.6e12, 2.4e12, 2.5e-6}};
+// full kernel names (tile configuration, then the A mode: 0 dense, 1 implicit conv)
+const char* const kNames[3][2] = {{"gemm_kernel<256,128,4,2,64,2,0>", "gemm_kernel<256,128,4,2,64,2,1>"},
+                                  {"gemm_kernel<128,128,2,2,64,2,0>", "gemm_kernel<128,128,2,2,64,2,1>"},
+                                  {"gemm_kernel<128,64,2,2,64,3,0>", "gemm_kernel<128,64,2,2,64,3,1>"}};
 
 int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
@@ -546,7 +549,7 @@ void plan(const GemmArgs& a, int& ci, int& splits, int& kps) {
 const char* gemm_kernel_name(const GemmArgs& a) {
     int ci, splits, kps;
     plan(a, ci, splits, kps);
-    return kCfgs[ci].name;
+    return kNames[ci][a.amode == A_CONV3];
 }
 
 size_t gemm_workspace_bytes(const GemmArgs& a) {
@@ -587,7 +590,7 @@ hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s) {
     const double part_bytes = splits > 1 ? 4.0 * splits * a.M * a.N : 0.0;
     const double flops = 2.0 * a.M * a.N * a.K;
     const double k_bytes = a_bytes + 2.0 * a.N * a.K + (splits > 1 ? part_bytes : out_bytes);
-    launch_timed(kCfgs[ci].name, flops, k_bytes, [&] {
+    launch_timed(kNames[ci][a.amode == A_CONV3], flops, k_bytes, [&] {
         if (a.amode == A_DENSE) launch_cfg<A_DENSE>(ci, grid, a, s);
         else launch_cfg<A_CONV3>(ci, grid, a, s);
     });
