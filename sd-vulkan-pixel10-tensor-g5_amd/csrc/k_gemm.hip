@@ -60,6 +60,34 @@ __device__ __forceinline__ void wait_vmcnt_lgkm0() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0x0 << 8) | ((N >> 4) << 14));
 }
 
+// Sum the per-thread column statistics of a block over the threads that own the same
+// 8 columns (thread t owns chunk t % cpr; chunk c covers columns col0 + 8c ..) through
+// LDS and add them to the per-(image, channel) fp64 statistics, one atomic per value,
+// the sums spread over all threads.  red must hold blockDim.x * 32 floats and be free
+// (the caller's last LDS use is complete after the first barrier here).
+__device__ __forceinline__ void stats_flush(const GemmArgs& a, const float (&st)[2][2][8], int b0,
+                                            int m_last, int col0, int cpr, float* red) {
+    const int tid = threadIdx.x, nth = blockDim.x;
+    __syncthreads();
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) red[tid * 32 + sl * 16 + q * 8 + e] = st[sl][q][e];
+    __syncthreads();
+    const int nslot = m_last / a.stats_hw != b0 ? 2 : 1;
+    // value v of chunk c: slot v / 16, sum (0) or sum of squares (1) = (v / 8) % 2, column v % 8
+    for (int idx = tid; idx < cpr * 32; idx += nth) {
+        const int c = idx >> 5, v = idx & 31;
+        const int col = col0 + c * 8 + (v & 7);
+        if ((v >> 4) >= nslot || col >= a.N) continue;
+        float t = 0.f;
+        for (int r = c; r < nth; r += cpr) t += red[r * 32 + v];
+        atomicAdd(&a.stats[((int64_t)(b0 + (v >> 4)) * a.N + col) * 2 + ((v >> 3) & 1)], (double)t);
+    }
+}
+
 // Sum split-K partials and apply the epilogue.  Vector path: 8 output columns
 // (N % 8 == 0 and not NCHW); scalar path: one element.
 __device__ __forceinline__ void reduce_scalar(const GemmArgs& a, int m, int nout) {
@@ -73,33 +101,70 @@ __device__ __forceinline__ void reduce_scalar(const GemmArgs& a, int m, int nout
     epi_store(a, m, n, v, g, nout);
 }
 
-__device__ __forceinline__ void reduce_vec8(const GemmArgs& a, int m, int nout) {
+// Returns the stored fp16 values (OUT_F16).
+__device__ __forceinline__ uint4 reduce_vec8(const GemmArgs& a, int m, int nout) {
     const int64_t mn = (int64_t)a.M * a.N;
     const int n = a.geglu ? (nout >> 5) * 64 + (nout & 31) : nout;
+    // epilogue operands first: bias (+ gate bias), time bias, residual
     float v[8], g[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) { v[e] = 0.f; g[e] = 0.f; }
-    for (int z = 0; z < a.splits; ++z) {
-        const float* p = a.partial + z * mn + (int64_t)m * a.N + n;
-        const float4 p0 = *(const float4*)p, p1 = *(const float4*)(p + 4);
-        v[0] += p0.x; v[1] += p0.y; v[2] += p0.z; v[3] += p0.w;
-        v[4] += p1.x; v[5] += p1.y; v[6] += p1.z; v[7] += p1.w;
+    if (a.bias) {
+        const uint4 bv = *(const uint4*)(a.bias + n);
+        const f16* bh = (const f16*)&bv;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (float)bh[e];
         if (a.geglu) {
-            const float4 q0 = *(const float4*)(p + 32), q1 = *(const float4*)(p + 36);
-            g[0] += q0.x; g[1] += q0.y; g[2] += q0.z; g[3] += q0.w;
-            g[4] += q1.x; g[5] += q1.y; g[6] += q1.z; g[7] += q1.w;
+            const uint4 gv = *(const uint4*)(a.bias + n + 32);
+            const f16* gh = (const f16*)&gv;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) g[e] = (float)gh[e];
+        }
+    }
+    if (a.bias2) {
+        const float4 c0 = *(const float4*)(a.bias2 + n), c1 = *(const float4*)(a.bias2 + n + 4);
+        v[0] += c0.x; v[1] += c0.y; v[2] += c0.z; v[3] += c0.w;
+        v[4] += c1.x; v[5] += c1.y; v[6] += c1.z; v[7] += c1.w;
+        if (a.geglu) {
+            const float4 d0 = *(const float4*)(a.bias2 + n + 32), d1 = *(const float4*)(a.bias2 + n + 36);
+            g[0] += d0.x; g[1] += d0.y; g[2] += d0.z; g[3] += d0.w;
+            g[4] += d1.x; g[5] += d1.y; g[6] += d1.z; g[7] += d1.w;
         }
     }
     uint4 rr = make_uint4(0, 0, 0, 0);
     if (a.res) rr = *(const uint4*)(a.res + (int64_t)m * a.ldr + nout);
+    // splits in rounds of 4 whose loads are all issued before any is added (the last
+    // round re-reads split splits-1 and weights the repeats 0)
+    const float* pb = a.partial + (int64_t)m * a.N + n;
+    for (int z0 = 0; z0 < a.splits; z0 += 4) {
+        float4 p0[4], p1[4], q0[4], q1[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const float* p = pb + min(z0 + u, a.splits - 1) * mn;
+            p0[u] = *(const float4*)p;
+            p1[u] = *(const float4*)(p + 4);
+            if (a.geglu) {
+                q0[u] = *(const float4*)(p + 32);
+                q1[u] = *(const float4*)(p + 36);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (z0 + u >= a.splits) break;
+            v[0] += p0[u].x; v[1] += p0[u].y; v[2] += p0[u].z; v[3] += p0[u].w;
+            v[4] += p1[u].x; v[5] += p1[u].y; v[6] += p1[u].z; v[7] += p1[u].w;
+            if (a.geglu) {
+                g[0] += q0[u].x; g[1] += q0[u].y; g[2] += q0[u].z; g[3] += q0[u].w;
+                g[4] += q1[u].x; g[5] += q1[u].y; g[6] += q1[u].z; g[7] += q1[u].w;
+            }
+        }
+    }
     const f16* rh = (const f16*)&rr;
     float o[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-        float x = v[e], gt = g[e];
-        if (a.bias) { x += (float)a.bias[n + e]; if (a.geglu) gt += (float)a.bias[n + 32 + e]; }
-        if (a.bias2) { x += a.bias2[n + e]; if (a.geglu) gt += a.bias2[n + 32 + e]; }
-        if (a.geglu) x *= gelu_erf(gt);
+        float x = v[e];
+        if (a.geglu) x *= gelu_erf(g[e]);
         if (a.res) x += (float)rh[e];
         o[e] = x;
     }
@@ -109,11 +174,45 @@ __device__ __forceinline__ void reduce_vec8(const GemmArgs& a, int m, int nout) 
 #pragma unroll
         for (int e = 0; e < 8; ++e) oh[e] = (f16)o[e];
         *(uint4*)((f16*)a.C + (int64_t)m * a.ldc + nout) = ov;
-    } else {
-        float* cp = (float*)a.C + (int64_t)m * a.ldc + nout;
-        *(float4*)cp = make_float4(o[0], o[1], o[2], o[3]);
-        *(float4*)(cp + 4) = make_float4(o[4], o[5], o[6], o[7]);
+        return ov;
     }
+    float* cp = (float*)a.C + (int64_t)m * a.ldc + nout;
+    *(float4*)cp = make_float4(o[0], o[1], o[2], o[3]);
+    *(float4*)(cp + 4) = make_float4(o[4], o[5], o[6], o[7]);
+    return make_uint4(0, 0, 0, 0);
+}
+
+// Split-K reduce for outputs whose channel statistics are needed: block = 8 column
+// chunks (64 columns) x 32 row phases, each thread `rpt` rows (rows of a block:
+// 32 * rpt <= 64 <= stats_hw, so a block spans at most two images).
+__global__ __launch_bounds__(256) void splitk_reduce_stats_kernel(GemmArgs a, int rpt) {
+    const int tid = threadIdx.x;
+    const int col0 = blockIdx.x * 64;
+    const int n = col0 + (tid & 7) * 8;
+    const int mb = blockIdx.y * 32 * rpt;
+    const int b0 = mb / a.stats_hw;
+    float st[2][2][8];
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) { st[sl][0][e] = 0.f; st[sl][1][e] = 0.f; }
+    if (n < a.N) {
+        for (int j = 0; j < rpt; ++j) {
+            const int m = mb + (tid >> 3) + 32 * j;
+            if (m >= a.M) break;
+            const uint4 o = reduce_vec8(a, m, n);  // stored fp16 values
+            const f16* oh = (const f16*)&o;
+            const bool s1 = m / a.stats_hw != b0;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float f = (float)oh[e];
+                if (s1) { st[1][0][e] += f; st[1][1][e] += f * f; }
+                else { st[0][0][e] += f; st[0][1][e] += f * f; }
+            }
+        }
+    }
+    __shared__ float red[256 * 32];
+    stats_flush(a, st, b0, min(a.M, mb + 32 * rpt) - 1, col0, 8, red);
 }
 
 __global__ void splitk_reduce_kernel(GemmArgs a) {
@@ -396,6 +495,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
     constexpr int PR = WM * 32;  // staged rows per pass
     constexpr int CST = NT + 4;  // padded fp32 row stride
     static_assert(PR * CST * 4 <= NS * STAGE * 2, "C pass fits the operand LDS");
+    static_assert(NTH * 32 * 4 <= NS * STAGE * 2, "statistics flush fits the operand LDS");
     float* Cs = (float*)smem;
     const bool narrow = a.out_mode == OUT_F32_NCHW || (a.N & 7);
     const int NTO = NT / (a.geglu ? 2 : 1);  // output columns of this tile
@@ -431,6 +531,15 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
         }
     }
     constexpr int MAXR = PR * (NT / 8) / NTH;  // staged rows per thread per pass (non-GEGLU)
+    // per-channel output statistics (GroupNorm of the consumer): this thread's 8
+    // columns over its rows, for the tile's first image (slot 0) and the next (slot 1)
+    const bool do_st = a.stats != nullptr && !narrow;
+    const int st_b0 = do_st ? m0 / a.stats_hw : 0;
+    float st[2][2][8];
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) { st[sl][0][e] = 0.f; st[sl][1][e] = 0.f; }
 #pragma unroll
     for (int ip = 0; ip < FM; ++ip) {
         __syncthreads();
@@ -488,6 +597,15 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) oh[e] = (f16)v[e];
                 *(uint4*)((f16*)a.C + (int64_t)m * a.ldc + nout) = o;
+                if (do_st) {
+                    const bool s1 = m / a.stats_hw != st_b0;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const float f = (float)oh[e];
+                        if (s1) { st[1][0][e] += f; st[1][1][e] += f * f; }
+                        else { st[0][0][e] += f; st[0][1][e] += f * f; }
+                    }
+                }
             } else {
                 float* cp = (float*)a.C + (int64_t)m * a.ldc + nout;
                 *(float4*)cp = make_float4(v[0], v[1], v[2], v[3]);
@@ -495,6 +613,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
             }
         }
     }
+    if (do_st) stats_flush(a, st, st_b0, min(a.M, m0 + MT) - 1, n0, cpr, (float*)smem);
 }
 
 namespace {
@@ -516,6 +635,10 @@ const char* const kNames[3][2] = {{"gemm_kernel<256,128,4,2,64,2,0>", "gemm_kern
 
 int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
+// The epilogue keeps output statistics for two images per tile: the MT rows of a tile
+// (MT-aligned) must not reach a third image.
+bool stats_tile_ok(int mt, int hw) { return hw >= mt || mt == 2 * hw; }
+
 // Pick the tile shape and split-K factor with the lowest modelled time.  Blocks are
 // spread evenly over the 256 CUs; the busiest CU runs its blocks two at a time where
 // the tile allows two per CU (a lone block cannot keep a CU busy: rate1 < rate2),
@@ -528,6 +651,7 @@ void plan(const GemmArgs& a, int& ci, int& splits, int& kps) {
     for (int c = 0; c < 3; ++c) {
         const Cfg& g = kCfgs[c];
         if (a.geglu && g.nt < 128) continue;  // GEGLU pairs 32-column blocks within a 64-wide wave tile
+        if (a.stats && !stats_tile_ok(g.mt, a.stats_hw)) continue;
         const int tiles = ceil_div(a.M, g.mt) * ceil_div(a.N, g.nt);
         static const int cand[] = {1, 2, 3, 4, 6, 8, 12, 16, 24, 32};
         for (int s : cand) {
@@ -545,6 +669,8 @@ void plan(const GemmArgs& a, int& ci, int& splits, int& kps) {
     }
 }
 }  // namespace
+
+bool gemm_stats_supported(int hw) { return stats_tile_ok(128, hw); }
 
 const char* gemm_kernel_name(const GemmArgs& a) {
     int ci, splits, kps;
@@ -580,6 +706,9 @@ hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s) {
         return hipErrorInvalidValue;
     if (a.amode == A_CONV3 && 2 * (int64_t)a.Bn * a.Hin * a.Win * a.Cin > lim) return hipErrorInvalidValue;
     const Cfg& g = kCfgs[ci];
+    if (a.stats && (a.out_mode != OUT_F16 || a.geglu || (a.N & 7) || a.stats_hw < 64 ||
+                    !stats_tile_ok(g.mt, a.stats_hw)))
+        return hipErrorInvalidValue;
     dim3 grid(ceil_div(a.M, g.mt) * ceil_div(a.N, g.nt), 1, splits);
     // algorithmic traffic: A once (the conv source image, not its im2col), W once, output
     // (+ residual) once; a split pays its fp32 partials out and back
@@ -598,9 +727,19 @@ hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s) {
     if (e != hipSuccess || splits == 1) return e;
     const bool vec = a.out_mode != OUT_F32_NCHW && (a.N & 7) == 0;
     const int64_t total = (int64_t)a.M * (vec ? nout / 8 : nout);
-    launch_timed("splitk_reduce_kernel", 0.0, part_bytes + out_bytes, [&] {
-        hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, a);
-    });
+    if (a.stats) {
+        // two rows per thread where that still leaves a few blocks per CU
+        const int cb = ceil_div(a.N, 64);
+        const int rpt = (long)cb * ceil_div(a.M, 64) >= 1024 ? 2 : 1;
+        const dim3 grid((unsigned)cb, (unsigned)ceil_div(a.M, 32 * rpt));
+        launch_timed("splitk_reduce_stats_kernel", 0.0, part_bytes + out_bytes, [&] {
+            hipLaunchKernelGGL(splitk_reduce_stats_kernel, grid, dim3(256), 0, s, a, rpt);
+        });
+    } else {
+        launch_timed("splitk_reduce_kernel", 0.0, part_bytes + out_bytes, [&] {
+            hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, a);
+        });
+    }
     return hipGetLastError();
 }
 

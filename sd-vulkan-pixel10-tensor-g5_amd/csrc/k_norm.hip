@@ -109,47 +109,100 @@ __global__ __launch_bounds__(GN_THREADS) void gn_stats_kernel(const f16* x, cons
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }
 
+// Apply y = act((x - mean_g) * rstd_g * gamma + beta) over GNA_VEC vectors of 8
+// channels of one image per block (vector i: pixel i / V, channels 8 * (i % V) ..).
+// All of a thread's loads (data, gamma, beta) are issued before the group statistics
+// are formed, so their latencies overlap.
+// CST = false: acc holds the per-group sums [B][G][2] of gn_stats_kernel.
+// CST = true: acc and st2 hold per-channel sums [B][C1][2] and [B][C2][2] written by
+// the GEMM epilogues that produced x and x2; 8 threads add up each group's channels.
+static constexpr int GNA_VPT = 4;
+static constexpr int GNA_VEC = GN_THREADS * GNA_VPT;
+template <bool CST>
 __global__ __launch_bounds__(GN_THREADS) void gn_apply_kernel(const f16* x, const f16* x2, int C1,
                                                               int C2, const f16* gamma,
-                                                              const f16* beta, f16* y, int HW,
-                                                              int P, int G, float eps, int silu,
-                                                              const double* acc) {
+                                                              const f16* beta, f16* y, int HW, int G,
+                                                              float eps, int silu, const double* acc,
+                                                              const double* st2) {
     const int C = C1 + C2, V = C / 8, cpg = C / G;
-    const int chunk = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-    __shared__ float tab[2 * GN_MAXC];
+    const int b = blockIdx.y, tid = threadIdx.x;
+    const int nvec = HW * V;  // < 2^31 (checked by the launchers)
+    const int64_t pix0 = (int64_t)b * HW;
+    // Loads are unconditional (index clamped to the last vector) and branch-free, so
+    // that all of them are in flight together.
+    uint4 raw[GNA_VPT], gv[GNA_VPT], bv[GNA_VPT];
+    int pv[GNA_VPT], cv[GNA_VPT];  // pixel within the image, first channel
+    unsigned valid = 0;
+#pragma unroll
+    for (int k = 0; k < GNA_VPT; ++k) {
+        int i = blockIdx.x * GNA_VEC + k * GN_THREADS + tid;
+        if (i < nvec) valid |= 1u << k;
+        i = min(i, nvec - 1);
+        const int p = i / V;
+        const int ch = (i - p * V) * 8;
+        pv[k] = p;
+        cv[k] = ch;
+        const f16* src = ch < C1 ? x + (pix0 + p) * C1 + ch : x2 + (pix0 + p) * C2 + (ch - C1);
+        raw[k] = *(const uint4*)src;
+        gv[k] = *(const uint4*)(gamma + ch);
+        bv[k] = *(const uint4*)(beta + ch);
+    }
     __shared__ float s_mean[GN_MAXG], s_rstd[GN_MAXG];
-    if (tid < G) {
-        const double n = (double)HW * cpg;
+    const double n = (double)HW * cpg;
+    if (CST) {
+        const int g = tid / 8, sub = tid % 8;
+        double ga = 0.0, gq = 0.0;
+        if (g < G) {
+            // 4 channels per round, loads issued together (clamped, weighted 0 / 1)
+            for (int i0 = sub; i0 < cpg; i0 += 32) {
+                double2 qv[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int c = g * cpg + min(i0 + 8 * u, cpg - 1);
+                    const double* q = c < C1 ? acc + ((int64_t)b * C1 + c) * 2 : st2 + ((int64_t)b * C2 + (c - C1)) * 2;
+                    qv[u] = *(const double2*)q;
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (i0 + 8 * u < cpg) { ga += qv[u].x; gq += qv[u].y; }
+            }
+        }
+#pragma unroll
+        for (int off = 1; off < 8; off <<= 1) {
+            ga += __shfl_xor(ga, off);
+            gq += __shfl_xor(gq, off);
+        }
+        if (g < G && sub == 0) {
+            const double mean = ga / n;
+            const double var = fmax(gq / n - mean * mean, 0.0);
+            s_mean[g] = (float)mean;
+            s_rstd[g] = (float)(1.0 / sqrt(var + (double)eps));
+        }
+    } else if (tid < G) {
         const double mean = acc[(b * G + tid) * 2 + 0] / n;
         const double var = fmax(acc[(b * G + tid) * 2 + 1] / n - mean * mean, 0.0);
         s_mean[tid] = (float)mean;
         s_rstd[tid] = (float)(1.0 / sqrt(var + (double)eps));
     }
     __syncthreads();
-    for (int c = tid; c < C; c += GN_THREADS) {
-        const int gg = c / cpg;
-        const float sc = s_rstd[gg] * (float)gamma[c];
-        tab[c] = sc;
-        tab[C + c] = (float)beta[c] - s_mean[gg] * sc;
-    }
-    __syncthreads();
-    const int p0 = chunk * P;
-    const int pn = min(P, HW - p0);
-    const int64_t pixb = (int64_t)b * HW + p0;
-    for (int i = tid; i < pn * V; i += GN_THREADS) {
-        const int p = i / V, v = i - p * V;
-        const uint4 raw = load_src(x, x2, C1, C2, pixb + p, v * 8);
-        const f16* hv = (const f16*)&raw;
+#pragma unroll
+    for (int k = 0; k < GNA_VPT; ++k) {
+        if (!(valid >> k & 1)) continue;
+        const f16* hv = (const f16*)&raw[k];
+        const f16* hg = (const f16*)&gv[k];
+        const f16* hb = (const f16*)&bv[k];
+        int g = cv[k] / cpg, nb = (g + 1) * cpg;  // group of the next channel, its end
         uint4 outv;
         f16* ov = (f16*)&outv;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const int c = v * 8 + e;
-            float z = (float)hv[e] * tab[c] + tab[C + c];
+            if (cv[k] + e >= nb) { ++g; nb += cpg; }
+            const float sc = s_rstd[g] * (float)hg[e];
+            float z = ((float)hv[e] - s_mean[g]) * sc + (float)hb[e];
             if (silu) z = silu_f(z);
             ov[e] = (f16)z;
         }
-        *(uint4*)(y + (pixb + p) * C + v * 8) = outv;
+        *(uint4*)(y + (pix0 + pv[k]) * C + cv[k]) = outv;
     }
 }
 
@@ -270,7 +323,8 @@ hipError_t groupnorm_launch(const f16* x, const f16* x2, int C1, int C2, const f
                             const f16* beta, f16* y, int B, int HW, int G, float eps, int silu,
                             double* acc, hipStream_t s) {
     const int C = C1 + C2;
-    if (G > GN_MAXG || C > GN_MAXC || C % G || C % 8 || C1 % 8 || (C2 && !x2)) return hipErrorInvalidValue;
+    if (G > GN_MAXG || C > GN_MAXC || C % G || C % 8 || C1 % 8 || (C2 && !x2) || (int64_t)HW * C >= 0x7fffffff)
+        return hipErrorInvalidValue;
     const double xbytes = 2.0 * B * HW * C;
     const int cpg = C / G;
     const int sweep = cpg % 2 == 0 ? GNF_THREADS / (cpg / 2) : 0;  // pixels per block sweep
@@ -299,9 +353,26 @@ hipError_t groupnorm_launch(const f16* x, const f16* x2, int C1, int C2, const f
     });
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    launch_timed("gn_apply_kernel", 0.0, 2.0 * xbytes, [&] {
-        hipLaunchKernelGGL(gn_apply_kernel, dim3(g.nchunk, B), dim3(GN_THREADS), 0, s, x, x2, C1, C2, gamma,
-                           beta, y, HW, g.P, G, eps, silu, (const double*)acc);
+    const dim3 agrid((unsigned)(((int64_t)HW * (C / 8) + GNA_VEC - 1) / GNA_VEC), B);
+    launch_timed("gn_apply_kernel<0>", 0.0, 2.0 * xbytes, [&] {
+        hipLaunchKernelGGL(gn_apply_kernel<false>, agrid, dim3(GN_THREADS), 0, s, x, x2, C1, C2, gamma, beta, y,
+                           HW, G, eps, silu, (const double*)acc, (const double*)nullptr);
+    });
+    return hipGetLastError();
+}
+
+hipError_t groupnorm_apply_stats_launch(const f16* x, const f16* x2, int C1, int C2, const double* st1,
+                                        const double* st2, const f16* gamma, const f16* beta, f16* y,
+                                        int B, int HW, int G, float eps, int silu, hipStream_t s) {
+    const int C = C1 + C2;
+    if (G > GN_MAXG || C > GN_MAXC || C % G || C % 8 || C1 % 8 || (C2 && (!x2 || !st2)) || !st1 ||
+        (int64_t)HW * C >= 0x7fffffff)
+        return hipErrorInvalidValue;
+    const double xbytes = 2.0 * B * HW * C;
+    const dim3 agrid((unsigned)(((int64_t)HW * (C / 8) + GNA_VEC - 1) / GNA_VEC), B);
+    launch_timed("gn_apply_kernel<1>", 0.0, 2.0 * xbytes, [&] {
+        hipLaunchKernelGGL(gn_apply_kernel<true>, agrid, dim3(GN_THREADS), 0, s, x, x2, C1, C2, gamma, beta, y, HW,
+                           G, eps, silu, st1, st2);
     });
     return hipGetLastError();
 }

@@ -66,7 +66,17 @@ struct GemmArgs {
     float* partial;     // [splits, M, N] fp32 (null: no split)
     int splits;
     int k_per_split;    // multiple of the K tile
+    // Optional per-channel statistics of the stored fp16 output, for a GroupNorm that
+    // reads it: stats[b][n] += (sum, sum of squares) over the rows m of image
+    // b = m / stats_hw.  Must be zero on entry.  fp16 output, no GEGLU, N % 8 == 0,
+    // stats_hw >= 64 and gemm_stats_supported(stats_hw).
+    double* stats;
+    int stats_hw;
 };
+
+// Whether a GEMM can produce output statistics for images of `hw` rows (some tile
+// shape keeps each tile within two images).
+bool gemm_stats_supported(int hw);
 
 // Picks the tile shape and split-K factor; returns the fp32 workspace bytes the
 // launch needs (0 if none).  `ws` may be null when the return value is 0.
@@ -95,6 +105,11 @@ size_t groupnorm_acc_bytes(int B, int G);
 hipError_t groupnorm_launch(const f16* x, const f16* x2, int C1, int C2, const f16* gamma,
                             const f16* beta, f16* y, int B, int HW, int G, float eps, int silu,
                             double* acc, hipStream_t s);
+// GroupNorm apply from per-channel statistics produced by the GEMMs that wrote x and
+// x2 (GemmArgs::stats: [B][C1][2] and [B][C2][2] fp64 sums and sums of squares).
+hipError_t groupnorm_apply_stats_launch(const f16* x, const f16* x2, int C1, int C2, const double* st1,
+                                        const double* st2, const f16* gamma, const f16* beta, f16* y,
+                                        int B, int HW, int G, float eps, int silu, hipStream_t s);
 // Clear `bytes` (rounded up to 16) with a fill kernel (graph-safe, no memset node).
 hipError_t zero_launch(void* p, size_t bytes, hipStream_t s);
 hipError_t layernorm_launch(const f16* x, const f16* gamma, const f16* beta, f16* y, int T, int C,

@@ -61,6 +61,8 @@ struct Exec {
     float* gemm_ws = nullptr;
     size_t gemm_ws_need = 0;
     double* gn_acc = nullptr;  // next free GroupNorm accumulator slot (zeroed per forward)
+    double* st_next = nullptr;  // per-channel output statistics pool (zeroed per forward)
+    double* st_end = nullptr;
     hipError_t err = hipSuccess;
     EventTimer* timer = nullptr;  // eager profiling only
 
@@ -115,14 +117,38 @@ static GemmArgs conv3_args(const f16* x, int B, int Hin, int Win, int Cin, int C
     return a;
 }
 
-static void groupnorm(Exec& E, const f16* x, const f16* x2, int C1, int C2, const f16* g,
-                      const f16* b, f16* y, int HW, int silu) {
-    double* acc = E.gn_acc;
-    E.gn_acc += (size_t)E.B * kGroups * 2;
+// An activation with, when its producing GEMM kept them, the per-channel sums and sums
+// of squares [B][C][2] of its values (for the GroupNorm that reads it).
+struct Act {
+    const f16* p;
+    const double* st;
+};
+
+// Statistics slot for a GEMM output of N channels over images of HW pixels, or null
+// (then the GroupNorm that reads the output computes its own statistics).
+static void want_stats(Exec& E, GemmArgs& a, int HW) {
+    const size_t n = (size_t)E.B * a.N * 2;
+    if (!gemm_stats_supported(HW) || E.st_next == nullptr || E.st_next + n > E.st_end) return;
+    a.stats = E.st_next;
+    a.stats_hw = HW;
+    E.st_next += n;
+}
+
+static void groupnorm(Exec& E, Act x, Act x2, int C1, int C2, const f16* g, const f16* b, f16* y, int HW,
+                      int silu) {
     char shape[48];
     snprintf(shape, sizeof shape, "HW=%d C=%d", HW, C1 + C2);
+    if (x.st && (C2 == 0 || x2.st)) {
+        E.run(silu ? "groupnorm_silu" : "groupnorm", [&] {
+            return groupnorm_apply_stats_launch(x.p, x2.p, C1, C2, x.st, x2.st, g, b, y, E.B, HW, kGroups, kEps,
+                                                silu, E.s);
+        }, shape);
+        return;
+    }
+    double* acc = E.gn_acc;
+    E.gn_acc += (size_t)E.B * kGroups * 2;
     E.run(silu ? "groupnorm_silu" : "groupnorm", [&] {
-        return groupnorm_launch(x, x2, C1, C2, g, b, y, E.B, HW, kGroups, kEps, silu, acc, E.s);
+        return groupnorm_launch(x.p, x2.p, C1, C2, g, b, y, E.B, HW, kGroups, kEps, silu, acc, E.s);
     }, shape);
 }
 
@@ -148,8 +174,7 @@ struct Fwd {
 static const f16* W(Exec& E, const std::string& n) { return E.c.wd(n); }
 
 // ResNet block (vk_engine.cpp:623-637).  x2 != null: input is concat(x, x2).
-static f16* resnet(Exec& E, const ResDesc& r, const f16* x, const f16* x2, int H, int Wd,
-                   const float* tproj) {
+static Act resnet(Exec& E, const ResDesc& r, Act x, Act x2, int H, int Wd, const float* tproj) {
     const int B = E.B, M = B * H * Wd, HW = H * Wd;
     f16* out = E.alloc<f16>((size_t)M * r.cout);
     const size_t mk = E.ar->mark();
@@ -157,42 +182,50 @@ static f16* resnet(Exec& E, const ResDesc& r, const f16* x, const f16* x2, int H
     groupnorm(E, x, x2, r.cin1, r.cin - r.cin1, W(E, r.pf + ".norm1.weight"), W(E, r.pf + ".norm1.bias"),
               h, HW, 1);
     f16* hc = E.alloc<f16>((size_t)M * r.cout);
+    Act hca{hc, nullptr};
     {
         GemmArgs a = conv3_args(h, B, H, Wd, r.cin, r.cout, 1, 0, W(E, r.pf + ".conv1.weight"), hc);
         a.bias = W(E, r.pf + ".conv1.bias");
         a.bias2 = tproj + r.tproj_off;  // + time_emb_proj(silu(temb)) broadcast (:627-630)
+        want_stats(E, a, HW);
+        hca.st = a.stats;
         gemm(E, "conv3x3", a);
     }
     f16* h2 = E.alloc<f16>((size_t)M * r.cout);
-    groupnorm(E, hc, nullptr, r.cout, 0, W(E, r.pf + ".norm2.weight"), W(E, r.pf + ".norm2.bias"), h2,
-              HW, 1);
-    const f16* res = x;
+    groupnorm(E, hca, Act{nullptr, nullptr}, r.cout, 0, W(E, r.pf + ".norm2.weight"),
+              W(E, r.pf + ".norm2.bias"), h2, HW, 1);
+    const f16* res = x.p;
     if (r.cin != r.cout) {  // 1x1 shortcut over (possibly concatenated) input (:634)
         f16* sx = E.alloc<f16>((size_t)M * r.cout);
-        GemmArgs a = dense_args(x, r.cin1, M, r.cout, r.cin, W(E, r.pf + ".conv_shortcut.weight"), sx, r.cout);
-        if (x2) { a.A2 = x2; a.lda2 = r.cin - r.cin1; a.K1 = r.cin1; }
+        GemmArgs a = dense_args(x.p, r.cin1, M, r.cout, r.cin, W(E, r.pf + ".conv_shortcut.weight"), sx, r.cout);
+        if (x2.p) { a.A2 = x2.p; a.lda2 = r.cin - r.cin1; a.K1 = r.cin1; }
         a.bias = W(E, r.pf + ".conv_shortcut.bias");
         gemm(E, "conv1x1", a);
         res = sx;
     }
+    Act o{out, nullptr};
     {
         GemmArgs a = conv3_args(h2, B, H, Wd, r.cout, r.cout, 1, 0, W(E, r.pf + ".conv2.weight"), out);
         a.bias = W(E, r.pf + ".conv2.bias");
         a.res = res; a.ldr = r.cout;
+        want_stats(E, a, HW);
+        o.st = a.stats;
         gemm(E, "conv3x3", a);
     }
     E.ar->release(mk);
-    return out;
+    return o;
 }
 
 // Spatial transformer (vk_engine.cpp:640-675).  kv: fused cross K/V [B*L, kv_total].
-static f16* transformer(Exec& E, const XfDesc& t, const f16* x, int H, int Wd, const f16* kv, int L) {
+static Act transformer(Exec& E, const XfDesc& t, Act xa, int H, int Wd, const f16* kv, int L) {
+    const f16* x = xa.p;
     const int B = E.B, HW = H * Wd, M = B * HW, C = t.c;
     const std::string b = t.pf + ".transformer_blocks.0";
     f16* out = E.alloc<f16>((size_t)M * C);
     const size_t mk = E.ar->mark();
     f16* g = E.alloc<f16>((size_t)M * C);
-    groupnorm(E, x, nullptr, C, 0, W(E, t.pf + ".norm.weight"), W(E, t.pf + ".norm.bias"), g, HW, 0);
+    groupnorm(E, xa, Act{nullptr, nullptr}, C, 0, W(E, t.pf + ".norm.weight"), W(E, t.pf + ".norm.bias"), g,
+              HW, 0);
     f16* tt = E.alloc<f16>((size_t)M * C);  // token stream [B*HW, C] (no T_CH transpose: NHWC)
     {
         GemmArgs a = dense_args(g, C, M, C, C, W(E, t.pf + ".proj_in.weight"), tt, C);
@@ -238,24 +271,28 @@ static f16* transformer(Exec& E, const XfDesc& t, const f16* x, int H, int Wd, c
         a.res = tt; a.ldr = C;
         gemm(E, "linear", a);
     }
+    Act o{out, nullptr};
     {
         GemmArgs a = dense_args(tt, C, M, C, C, W(E, t.pf + ".proj_out.weight"), out, C);
         a.bias = W(E, t.pf + ".proj_out.bias");
         a.res = x; a.ldr = C;
+        want_stats(E, a, HW);
+        o.st = a.stats;
         gemm(E, "conv1x1", a);
     }
     E.ar->release(mk);
-    return out;
+    return o;
 }
 
-static f16* conv3_block(Exec& E, const std::string& pf, const f16* x, int H, int Wd, int Cin, int Cout,
-                        int stride, int ups) {
+static Act conv3_block(Exec& E, const std::string& pf, const f16* x, int H, int Wd, int Cin, int Cout,
+                       int stride, int ups) {
     GemmArgs a = conv3_args(x, E.B, H, Wd, Cin, Cout, stride, ups, W(E, pf + ".weight"), nullptr);
     f16* y = E.alloc<f16>((size_t)a.M * Cout);
     a.C = y;
     a.bias = W(E, pf + ".bias");
+    want_stats(E, a, a.Ho * a.Wo);
     gemm(E, "conv3x3", a);
-    return y;
+    return Act{y, a.stats};
 }
 
 // time MLP (vk_engine.cpp:716-717) + every resnet's time_emb_proj(silu(temb)) in
@@ -293,19 +330,29 @@ static void unet_core(Exec& E, const Fwd& F, const f16* lat, const float* temb32
                       float* out) {
     Ctx& c = E.c;
     const size_t mk0 = E.ar->mark();
-    // GroupNorm accumulators of this forward: 2 per resnet, 1 per transformer, conv_norm_out
+    // GroupNorm accumulators of this forward (2 per resnet, 1 per transformer, conv_norm_out)
+    // for GroupNorms that compute their own statistics, then the pool of per-channel
+    // statistics of the GEMM outputs that GroupNorms read (conv1 and conv2 of every
+    // resnet, every transformer's proj_out, conv_in and the 6 resampling convs);
+    // one clear for both.
     const size_t n_gn = 2 * c.resnets.size() + c.xfs.size() + 1;
-    const size_t acc_bytes = n_gn * groupnorm_acc_bytes(E.B, kGroups);
-    E.gn_acc = E.alloc<double>(acc_bytes / sizeof(double));
+    const size_t acc_n = n_gn * groupnorm_acc_bytes(E.B, kGroups) / sizeof(double);
+    size_t st_ch = 7 * 1280;
+    for (const ResDesc& r : c.resnets) st_ch += 2 * r.cout;
+    for (const XfDesc& t : c.xfs) st_ch += t.c;
+    const size_t st_n = (size_t)E.B * st_ch * 2;
+    E.gn_acc = E.alloc<double>(acc_n + st_n);
+    E.st_next = E.gn_acc + acc_n;
+    E.st_end = E.st_next + st_n;
     {
         void* p = E.gn_acc;
-        E.run("groupnorm", [&] { return zero_launch(p, acc_bytes, E.s); });
+        E.run("groupnorm", [&] { return zero_launch(p, (acc_n + st_n) * sizeof(double), E.s); });
     }
     const float* tproj = time_embed(E, temb320);
     int H = F.H, Wd = F.W;
-    struct Skip { const f16* p; int ch; };
+    struct Skip { Act a; int ch; };
     std::vector<Skip> skips;
-    const f16* x = conv3_block(E, "conv_in", lat, H, Wd, kLatCpad, 320, 1, 0);
+    Act x = conv3_block(E, "conv_in", lat, H, Wd, kLatCpad, 320, 1, 0);
     skips.push_back({x, 320});
     static const int bo[4] = {320, 640, 1280, 1280};
     static const int uo[4] = {1280, 1280, 640, 320};
@@ -314,7 +361,7 @@ static void unet_core(Exec& E, const Fwd& F, const f16* lat, const float* temb32
     for (int i = 0; i < 4; ++i) {
         for (int r = 0; r < 2; ++r) {
             snprintf(pf, sizeof pf, "down_blocks.%d.resnets.%d", i, r);
-            x = resnet(E, c.resnets[c.res_by_pf[pf]], x, nullptr, H, Wd, tproj);
+            x = resnet(E, c.resnets[c.res_by_pf[pf]], x, Act{nullptr, nullptr}, H, Wd, tproj);
             if (i < 3) {
                 snprintf(pf, sizeof pf, "down_blocks.%d.attentions.%d", i, r);
                 x = transformer(E, c.xfs[c.xf_by_pf[pf]], x, H, Wd, kv, F.L);
@@ -324,21 +371,21 @@ static void unet_core(Exec& E, const Fwd& F, const f16* lat, const float* temb32
         cprev = bo[i];
         if (i < 3) {
             snprintf(pf, sizeof pf, "down_blocks.%d.downsamplers.0.conv", i);
-            x = conv3_block(E, pf, x, H, Wd, bo[i], bo[i], 2, 0);
+            x = conv3_block(E, pf, x.p, H, Wd, bo[i], bo[i], 2, 0);
             H /= 2; Wd /= 2;
             skips.push_back({x, bo[i]});
         }
     }
-    x = resnet(E, c.resnets[c.res_by_pf["mid_block.resnets.0"]], x, nullptr, H, Wd, tproj);
+    x = resnet(E, c.resnets[c.res_by_pf["mid_block.resnets.0"]], x, Act{nullptr, nullptr}, H, Wd, tproj);
     x = transformer(E, c.xfs[c.xf_by_pf["mid_block.attentions.0"]], x, H, Wd, kv, F.L);
-    x = resnet(E, c.resnets[c.res_by_pf["mid_block.resnets.1"]], x, nullptr, H, Wd, tproj);
+    x = resnet(E, c.resnets[c.res_by_pf["mid_block.resnets.1"]], x, Act{nullptr, nullptr}, H, Wd, tproj);
     for (int i = 0; i < 4; ++i) {
         for (int r = 0; r < 3; ++r) {
             const Skip sk = skips.back();
             skips.pop_back();
             snprintf(pf, sizeof pf, "up_blocks.%d.resnets.%d", i, r);
             const ResDesc& rd = c.resnets[c.res_by_pf[pf]];
-            x = resnet(E, rd, x, sk.p, H, Wd, tproj);  // concat(prev, skip) read in place
+            x = resnet(E, rd, x, sk.a, H, Wd, tproj);  // concat(prev, skip) read in place
             cprev = uo[i];
             if (i > 0) {
                 snprintf(pf, sizeof pf, "up_blocks.%d.attentions.%d", i, r);
@@ -347,14 +394,15 @@ static void unet_core(Exec& E, const Fwd& F, const f16* lat, const float* temb32
         }
         if (i < 3) {
             snprintf(pf, sizeof pf, "up_blocks.%d.upsamplers.0.conv", i);
-            x = conv3_block(E, pf, x, H, Wd, uo[i], uo[i], 1, 1);
+            x = conv3_block(E, pf, x.p, H, Wd, uo[i], uo[i], 1, 1);
             H *= 2; Wd *= 2;
         }
     }
     (void)cprev;
     const int M = E.B * H * Wd;
     f16* gn = E.alloc<f16>((size_t)M * 320);
-    groupnorm(E, x, nullptr, 320, 0, c.wd("conv_norm_out.weight"), c.wd("conv_norm_out.bias"), gn, H * Wd, 1);
+    groupnorm(E, x, Act{nullptr, nullptr}, 320, 0, c.wd("conv_norm_out.weight"), c.wd("conv_norm_out.bias"), gn,
+              H * Wd, 1);
     GemmArgs a = conv3_args(gn, E.B, H, Wd, 320, kLatC, 1, 0, c.wd("conv_out.weight"), out);
     a.bias = c.wd("conv_out.bias");
     a.out_mode = OUT_F32_NCHW;
