@@ -101,95 +101,112 @@ __device__ __forceinline__ void reduce_scalar(const GemmArgs& a, int m, int nout
     epi_store(a, m, n, v, g, nout);
 }
 
-// Returns the stored fp16 values (OUT_F16).
-__device__ __forceinline__ uint4 reduce_vec8(const GemmArgs& a, int m, int nout) {
+// Sum the split-K partials of 8 output columns (nout ..) for R rows m[r] and apply the
+// epilogue; rows whose bit in `valid` is clear are read (m clamped by the caller) but
+// not stored.  Every load of a round of 4 splits over all R rows is issued before any
+// is added (the last round re-reads split splits-1 and weights the repeats 0), and
+// the bias / residual loads come first.  GG = false: no GEGLU.  ov[r] = the stored
+// fp16 values (OUT_F16).
+template <int R, bool GG>
+__device__ __forceinline__ void reduce_rows(const GemmArgs& a, const int (&m)[R], unsigned valid, int nout,
+                                            uint4 (&ov)[R]) {
+    // All loads are unconditional (absent operands read the zero page) and every
+    // loaded value is used, so the compiler keeps them in flight together.
     const int64_t mn = (int64_t)a.M * a.N;
-    const int n = a.geglu ? (nout >> 5) * 64 + (nout & 31) : nout;
-    // epilogue operands first: bias (+ gate bias), time bias, residual
-    float v[8], g[8];
+    const bool geglu = GG && a.geglu;
+    const int n = geglu ? (nout >> 5) * 64 + (nout & 31) : nout;
+    const f16* zh = (const f16*)g_zero_page;
+    const float* zf = (const float*)g_zero_page;
+    const uint4 bv = *(const uint4*)(a.bias ? a.bias + n : zh);
+    const uint4 gbv = *(const uint4*)(a.bias && geglu ? a.bias + n + 32 : zh);
+    const float4 c0 = *(const float4*)(a.bias2 ? a.bias2 + n : zf);
+    const float4 c1 = *(const float4*)(a.bias2 ? a.bias2 + n + 4 : zf);
+    const float4 d0 = *(const float4*)(a.bias2 && geglu ? a.bias2 + n + 32 : zf);
+    const float4 d1 = *(const float4*)(a.bias2 && geglu ? a.bias2 + n + 36 : zf);
+    uint4 rr[R];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) { v[e] = 0.f; g[e] = 0.f; }
-    if (a.bias) {
-        const uint4 bv = *(const uint4*)(a.bias + n);
+    for (int r = 0; r < R; ++r) rr[r] = *(const uint4*)(a.res ? a.res + (int64_t)m[r] * a.ldr + nout : zh);
+    float v[R][8], g[R][8];
+    {
         const f16* bh = (const f16*)&bv;
+        const f16* gh = (const f16*)&gbv;
+        const float cb[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+        const float db[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = (float)bh[e];
-        if (a.geglu) {
-            const uint4 gv = *(const uint4*)(a.bias + n + 32);
-            const f16* gh = (const f16*)&gv;
+        for (int r = 0; r < R; ++r)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) g[e] = (float)gh[e];
-        }
+            for (int e = 0; e < 8; ++e) {
+                v[r][e] = (float)bh[e] + cb[e];
+                g[r][e] = (float)gh[e] + db[e];
+            }
     }
-    if (a.bias2) {
-        const float4 c0 = *(const float4*)(a.bias2 + n), c1 = *(const float4*)(a.bias2 + n + 4);
-        v[0] += c0.x; v[1] += c0.y; v[2] += c0.z; v[3] += c0.w;
-        v[4] += c1.x; v[5] += c1.y; v[6] += c1.z; v[7] += c1.w;
-        if (a.geglu) {
-            const float4 d0 = *(const float4*)(a.bias2 + n + 32), d1 = *(const float4*)(a.bias2 + n + 36);
-            g[0] += d0.x; g[1] += d0.y; g[2] += d0.z; g[3] += d0.w;
-            g[4] += d1.x; g[5] += d1.y; g[6] += d1.z; g[7] += d1.w;
-        }
-    }
-    uint4 rr = make_uint4(0, 0, 0, 0);
-    if (a.res) rr = *(const uint4*)(a.res + (int64_t)m * a.ldr + nout);
-    // splits in rounds of 4 whose loads are all issued before any is added (the last
-    // round re-reads split splits-1 and weights the repeats 0)
-    const float* pb = a.partial + (int64_t)m * a.N + n;
     for (int z0 = 0; z0 < a.splits; z0 += 4) {
-        float4 p0[4], p1[4], q0[4], q1[4];
+        float4 p0[R][4], p1[R][4], q0[GG ? R : 1][4], q1[GG ? R : 1][4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float* p = a.partial + min(z0 + u, a.splits - 1) * mn + (int64_t)m[r] * a.N + n;
+                p0[r][u] = *(const float4*)p;
+                p1[r][u] = *(const float4*)(p + 4);
+                if (GG) {
+                    q0[GG ? r : 0][u] = *(const float4*)(geglu ? p + 32 : zf);
+                    q1[GG ? r : 0][u] = *(const float4*)(geglu ? p + 36 : zf);
+                }
+            }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const float* p = pb + min(z0 + u, a.splits - 1) * mn;
-            p0[u] = *(const float4*)p;
-            p1[u] = *(const float4*)(p + 4);
-            if (a.geglu) {
-                q0[u] = *(const float4*)(p + 32);
-                q1[u] = *(const float4*)(p + 36);
-            }
-        }
+            const bool use = z0 + u < a.splits;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            if (z0 + u >= a.splits) break;
-            v[0] += p0[u].x; v[1] += p0[u].y; v[2] += p0[u].z; v[3] += p0[u].w;
-            v[4] += p1[u].x; v[5] += p1[u].y; v[6] += p1[u].z; v[7] += p1[u].w;
-            if (a.geglu) {
-                g[0] += q0[u].x; g[1] += q0[u].y; g[2] += q0[u].z; g[3] += q0[u].w;
-                g[4] += q1[u].x; g[5] += q1[u].y; g[6] += q1[u].z; g[7] += q1[u].w;
+            for (int r = 0; r < R; ++r) {
+                const float x[8] = {p0[r][u].x, p0[r][u].y, p0[r][u].z, p0[r][u].w,
+                                    p1[r][u].x, p1[r][u].y, p1[r][u].z, p1[r][u].w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[r][e] += use ? x[e] : 0.f;
+                if (GG) {
+                    const float4 x0 = q0[GG ? r : 0][u], x1 = q1[GG ? r : 0][u];
+                    const float y[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) g[r][e] += use ? y[e] : 0.f;
+                }
             }
         }
     }
-    const f16* rh = (const f16*)&rr;
-    float o[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        float x = v[e];
-        if (a.geglu) x *= gelu_erf(g[e]);
-        if (a.res) x += (float)rh[e];
-        o[e] = x;
-    }
-    if (a.out_mode == OUT_F16) {
-        uint4 ov;
-        f16* oh = (f16*)&ov;
+    for (int r = 0; r < R; ++r) {
+        const f16* rh = (const f16*)&rr[r];
+        float o[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) oh[e] = (f16)o[e];
-        *(uint4*)((f16*)a.C + (int64_t)m * a.ldc + nout) = ov;
-        return ov;
+        for (int e = 0; e < 8; ++e) {
+            float x = v[r][e];
+            if (geglu) x *= gelu_erf(g[r][e]);
+            if (a.res) x += (float)rh[e];
+            o[e] = x;
+        }
+        ov[r] = make_uint4(0, 0, 0, 0);
+        if (!(valid >> r & 1)) continue;
+        if (a.out_mode == OUT_F16) {
+            f16* oh = (f16*)&ov[r];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) oh[e] = (f16)o[e];
+            *(uint4*)((f16*)a.C + (int64_t)m[r] * a.ldc + nout) = ov[r];
+        } else {
+            float* cp = (float*)a.C + (int64_t)m[r] * a.ldc + nout;
+            *(float4*)cp = make_float4(o[0], o[1], o[2], o[3]);
+            *(float4*)(cp + 4) = make_float4(o[4], o[5], o[6], o[7]);
+        }
     }
-    float* cp = (float*)a.C + (int64_t)m * a.ldc + nout;
-    *(float4*)cp = make_float4(o[0], o[1], o[2], o[3]);
-    *(float4*)(cp + 4) = make_float4(o[4], o[5], o[6], o[7]);
-    return make_uint4(0, 0, 0, 0);
 }
 
 // Split-K reduce for outputs whose channel statistics are needed: block = 8 column
-// chunks (64 columns) x 32 row phases, each thread `rpt` rows (rows of a block:
-// 32 * rpt <= 64 <= stats_hw, so a block spans at most two images).
-__global__ __launch_bounds__(256) void splitk_reduce_stats_kernel(GemmArgs a, int rpt) {
+// chunks (64 columns) x 32 row phases, each thread SR rows (rows of a block:
+// 32 * SR = 64 <= stats_hw, so a block spans at most two images).
+static constexpr int SR = 2;
+__global__ __launch_bounds__(256) void splitk_reduce_stats_kernel(GemmArgs a) {
     const int tid = threadIdx.x;
     const int col0 = blockIdx.x * 64;
     const int n = col0 + (tid & 7) * 8;
-    const int mb = blockIdx.y * 32 * rpt;
+    const int mb = blockIdx.y * 32 * SR;
     const int b0 = mb / a.stats_hw;
     float st[2][2][8];
 #pragma unroll
@@ -197,12 +214,21 @@ __global__ __launch_bounds__(256) void splitk_reduce_stats_kernel(GemmArgs a, in
 #pragma unroll
         for (int e = 0; e < 8; ++e) { st[sl][0][e] = 0.f; st[sl][1][e] = 0.f; }
     if (n < a.N) {
-        for (int j = 0; j < rpt; ++j) {
-            const int m = mb + (tid >> 3) + 32 * j;
-            if (m >= a.M) break;
-            const uint4 o = reduce_vec8(a, m, n);  // stored fp16 values
-            const f16* oh = (const f16*)&o;
-            const bool s1 = m / a.stats_hw != b0;
+        int m[SR];
+        unsigned valid = 0;
+#pragma unroll
+        for (int j = 0; j < SR; ++j) {
+            const int mj = mb + (tid >> 3) + 32 * j;
+            if (mj < a.M) valid |= 1u << j;
+            m[j] = min(mj, a.M - 1);
+        }
+        uint4 o[SR];
+        reduce_rows<SR, false>(a, m, valid, n, o);
+#pragma unroll
+        for (int j = 0; j < SR; ++j) {
+            if (!(valid >> j & 1)) continue;
+            const f16* oh = (const f16*)&o[j];
+            const bool s1 = m[j] / a.stats_hw != b0;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const float f = (float)oh[e];
@@ -212,7 +238,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_stats_kernel(GemmArgs a, in
         }
     }
     __shared__ float red[256 * 32];
-    stats_flush(a, st, b0, min(a.M, mb + 32 * rpt) - 1, col0, 8, red);
+    stats_flush(a, st, b0, min(a.M, mb + 32 * SR) - 1, col0, 8, red);
 }
 
 __global__ void splitk_reduce_kernel(GemmArgs a) {
@@ -227,8 +253,9 @@ __global__ void splitk_reduce_kernel(GemmArgs a) {
     }
     const int cpr = nout_cols / 8;
     if (idx >= (int64_t)a.M * cpr) return;
-    const int m = (int)(idx / cpr);
-    reduce_vec8(a, m, (int)(idx - (int64_t)m * cpr) * 8);
+    const int m[1] = {(int)(idx / cpr)};
+    uint4 o[1];
+    reduce_rows<1, true>(a, m, 1u, (int)(idx - (int64_t)m[0] * cpr) * 8, o);
 }
 
 // Main loop: NS-stage LDS ring fed by global_load_lds_dwordx4 (direct to LDS, no
@@ -728,12 +755,9 @@ hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s) {
     const bool vec = a.out_mode != OUT_F32_NCHW && (a.N & 7) == 0;
     const int64_t total = (int64_t)a.M * (vec ? nout / 8 : nout);
     if (a.stats) {
-        // two rows per thread where that still leaves a few blocks per CU
-        const int cb = ceil_div(a.N, 64);
-        const int rpt = (long)cb * ceil_div(a.M, 64) >= 1024 ? 2 : 1;
-        const dim3 grid((unsigned)cb, (unsigned)ceil_div(a.M, 32 * rpt));
+        const dim3 grid((unsigned)ceil_div(a.N, 64), (unsigned)ceil_div(a.M, 32 * SR));
         launch_timed("splitk_reduce_stats_kernel", 0.0, part_bytes + out_bytes, [&] {
-            hipLaunchKernelGGL(splitk_reduce_stats_kernel, grid, dim3(256), 0, s, a, rpt);
+            hipLaunchKernelGGL(splitk_reduce_stats_kernel, grid, dim3(256), 0, s, a);
         });
     } else {
         launch_timed("splitk_reduce_kernel", 0.0, part_bytes + out_bytes, [&] {

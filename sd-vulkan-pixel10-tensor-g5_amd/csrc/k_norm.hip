@@ -109,15 +109,30 @@ __global__ __launch_bounds__(GN_THREADS) void gn_stats_kernel(const f16* x, cons
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }
 
-// Apply y = act((x - mean_g) * rstd_g * gamma + beta) over GNA_VEC vectors of 8
-// channels of one image per block (vector i: pixel i / V, channels 8 * (i % V) ..).
-// All of a thread's loads (data, gamma, beta) are issued before the group statistics
-// are formed, so their latencies overlap.
+// Apply y = act((x - mean_g) * rstd_g * gamma + beta) to one image per blockIdx.y.
+// The image is cut into chunks of GNA_VEC vectors of 8 channels (vector i: pixel
+// i / V, channels 8 * (i % V) ..); block x handles chunks x, x + gridDim.x, ... and
+// loads the next chunk while it writes the current one.  The first chunk's loads are
+// issued before the group statistics are formed, so their latencies overlap.
 // CST = false: acc holds the per-group sums [B][G][2] of gn_stats_kernel.
 // CST = true: acc and st2 hold per-channel sums [B][C1][2] and [B][C2][2] written by
 // the GEMM epilogues that produced x and x2; 8 threads add up each group's channels.
 static constexpr int GNA_VPT = 4;
 static constexpr int GNA_VEC = GN_THREADS * GNA_VPT;
+
+// Branch-free loads of one chunk (index clamped to the last vector of the image).
+__device__ __forceinline__ void gna_load(const f16* x, const f16* x2, int C1, int C2, int V, int nvec,
+                                         int64_t pix0, int chunk, uint4 (&raw)[GNA_VPT]) {
+#pragma unroll
+    for (int k = 0; k < GNA_VPT; ++k) {
+        const int i = min(chunk * GNA_VEC + k * GN_THREADS + (int)threadIdx.x, nvec - 1);
+        const int p = i / V;
+        const int ch = (i - p * V) * 8;
+        const f16* src = ch < C1 ? x + (pix0 + p) * C1 + ch : x2 + (pix0 + p) * C2 + (ch - C1);
+        raw[k] = *(const uint4*)src;
+    }
+}
+
 template <bool CST>
 __global__ __launch_bounds__(GN_THREADS) void gn_apply_kernel(const f16* x, const f16* x2, int C1,
                                                               int C2, const f16* gamma,
@@ -127,27 +142,20 @@ __global__ __launch_bounds__(GN_THREADS) void gn_apply_kernel(const f16* x, cons
     const int C = C1 + C2, V = C / 8, cpg = C / G;
     const int b = blockIdx.y, tid = threadIdx.x;
     const int nvec = HW * V;  // < 2^31 (checked by the launchers)
+    const int nchunk = (nvec + GNA_VEC - 1) / GNA_VEC;
     const int64_t pix0 = (int64_t)b * HW;
-    // Loads are unconditional (index clamped to the last vector) and branch-free, so
-    // that all of them are in flight together.
-    uint4 raw[GNA_VPT], gv[GNA_VPT], bv[GNA_VPT];
-    int pv[GNA_VPT], cv[GNA_VPT];  // pixel within the image, first channel
-    unsigned valid = 0;
+    uint4 raw[GNA_VPT];
+    gna_load(x, x2, C1, C2, V, nvec, pix0, blockIdx.x, raw);
+    // gamma / beta of the channel octets this thread turns into table entries
+    uint4 gv[2], bv[2];
 #pragma unroll
-    for (int k = 0; k < GNA_VPT; ++k) {
-        int i = blockIdx.x * GNA_VEC + k * GN_THREADS + tid;
-        if (i < nvec) valid |= 1u << k;
-        i = min(i, nvec - 1);
-        const int p = i / V;
-        const int ch = (i - p * V) * 8;
-        pv[k] = p;
-        cv[k] = ch;
-        const f16* src = ch < C1 ? x + (pix0 + p) * C1 + ch : x2 + (pix0 + p) * C2 + (ch - C1);
-        raw[k] = *(const uint4*)src;
-        gv[k] = *(const uint4*)(gamma + ch);
-        bv[k] = *(const uint4*)(beta + ch);
+    for (int j = 0; j < 2; ++j) {
+        const int o = min(tid + j * GN_THREADS, V - 1);
+        gv[j] = *(const uint4*)(gamma + o * 8);
+        bv[j] = *(const uint4*)(beta + o * 8);
     }
     __shared__ float s_mean[GN_MAXG], s_rstd[GN_MAXG];
+    __shared__ float4 tab[GN_MAXC / 2];  // per channel octet: 2 x (scale[4]), 2 x (shift[4])
     const double n = (double)HW * cpg;
     if (CST) {
         const int g = tid / 8, sub = tid % 8;
@@ -163,8 +171,11 @@ __global__ __launch_bounds__(GN_THREADS) void gn_apply_kernel(const f16* x, cons
                     qv[u] = *(const double2*)q;
                 }
 #pragma unroll
-                for (int u = 0; u < 4; ++u)
-                    if (i0 + 8 * u < cpg) { ga += qv[u].x; gq += qv[u].y; }
+                for (int u = 0; u < 4; ++u) {
+                    const bool use = i0 + 8 * u < cpg;
+                    ga += use ? qv[u].x : 0.0;
+                    gq += use ? qv[u].y : 0.0;
+                }
             }
         }
 #pragma unroll
@@ -186,24 +197,58 @@ __global__ __launch_bounds__(GN_THREADS) void gn_apply_kernel(const f16* x, cons
     }
     __syncthreads();
 #pragma unroll
-    for (int k = 0; k < GNA_VPT; ++k) {
-        if (!(valid >> k & 1)) continue;
-        const f16* hv = (const f16*)&raw[k];
-        const f16* hg = (const f16*)&gv[k];
-        const f16* hb = (const f16*)&bv[k];
-        int g = cv[k] / cpg, nb = (g + 1) * cpg;  // group of the next channel, its end
-        uint4 outv;
-        f16* ov = (f16*)&outv;
+    for (int j = 0; j < 2; ++j) {
+        const int o = tid + j * GN_THREADS;
+        if (o >= V) break;
+        const f16* hg = (const f16*)&gv[j];
+        const f16* hb = (const f16*)&bv[j];
+        float sc[8], sh[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            if (cv[k] + e >= nb) { ++g; nb += cpg; }
-            const float sc = s_rstd[g] * (float)hg[e];
-            float z = ((float)hv[e] - s_mean[g]) * sc + (float)hb[e];
-            if (silu) z = silu_f(z);
-            ov[e] = (f16)z;
+            const int g = (o * 8 + e) / cpg;
+            sc[e] = s_rstd[g] * (float)hg[e];
+            sh[e] = (float)hb[e] - s_mean[g] * sc[e];
         }
-        *(uint4*)(y + (pix0 + pv[k]) * C + cv[k]) = outv;
+        tab[o * 4 + 0] = make_float4(sc[0], sc[1], sc[2], sc[3]);
+        tab[o * 4 + 1] = make_float4(sc[4], sc[5], sc[6], sc[7]);
+        tab[o * 4 + 2] = make_float4(sh[0], sh[1], sh[2], sh[3]);
+        tab[o * 4 + 3] = make_float4(sh[4], sh[5], sh[6], sh[7]);
     }
+    __syncthreads();
+    for (int chunk = blockIdx.x; chunk < nchunk; chunk += gridDim.x) {
+        uint4 nxt[GNA_VPT];
+        const int cn = chunk + gridDim.x;
+        if (cn < nchunk) gna_load(x, x2, C1, C2, V, nvec, pix0, cn, nxt);
+#pragma unroll
+        for (int k = 0; k < GNA_VPT; ++k) {
+            const int i = chunk * GNA_VEC + k * GN_THREADS + tid;
+            if (i >= nvec) continue;
+            const int p = i / V, o = i - p * V;
+            const float4 s0 = tab[o * 4 + 0], s1 = tab[o * 4 + 1], h0 = tab[o * 4 + 2], h1 = tab[o * 4 + 3];
+            const float sc[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+            const float sh[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+            const f16* hv = (const f16*)&raw[k];
+            uint4 outv;
+            f16* ov = (f16*)&outv;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                float z = (float)hv[e] * sc[e] + sh[e];
+                if (silu) z = silu_f(z);
+                ov[e] = (f16)z;
+            }
+            *(uint4*)(y + (pix0 + p) * C + o * 8) = outv;
+        }
+#pragma unroll
+        for (int k = 0; k < GNA_VPT; ++k) raw[k] = nxt[k];
+    }
+}
+
+// Blocks per image for gn_apply_kernel: about 2048 blocks in all, each taking the
+// same number of chunks (+-1).
+static int gna_blocks(int HW, int C, int B) {
+    const int nchunk = (int)(((int64_t)HW * (C / 8) + GNA_VEC - 1) / GNA_VEC);
+    const int per = (nchunk * B + 2047) / 2048;  // chunks per block
+    return (nchunk + per - 1) / per;
 }
 
 __global__ void zero_kernel(uint4* p, int64_t n16) {
@@ -353,7 +398,7 @@ hipError_t groupnorm_launch(const f16* x, const f16* x2, int C1, int C2, const f
     });
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const dim3 agrid((unsigned)(((int64_t)HW * (C / 8) + GNA_VEC - 1) / GNA_VEC), B);
+    const dim3 agrid(gna_blocks(HW, C, B), B);
     launch_timed("gn_apply_kernel<0>", 0.0, 2.0 * xbytes, [&] {
         hipLaunchKernelGGL(gn_apply_kernel<false>, agrid, dim3(GN_THREADS), 0, s, x, x2, C1, C2, gamma, beta, y,
                            HW, G, eps, silu, (const double*)acc, (const double*)nullptr);
@@ -369,7 +414,7 @@ hipError_t groupnorm_apply_stats_launch(const f16* x, const f16* x2, int C1, int
         (int64_t)HW * C >= 0x7fffffff)
         return hipErrorInvalidValue;
     const double xbytes = 2.0 * B * HW * C;
-    const dim3 agrid((unsigned)(((int64_t)HW * (C / 8) + GNA_VEC - 1) / GNA_VEC), B);
+    const dim3 agrid(gna_blocks(HW, C, B), B);
     launch_timed("gn_apply_kernel<1>", 0.0, 2.0 * xbytes, [&] {
         hipLaunchKernelGGL(gn_apply_kernel<true>, agrid, dim3(GN_THREADS), 0, s, x, x2, C1, C2, gamma, beta, y, HW,
                            G, eps, silu, st1, st2);
