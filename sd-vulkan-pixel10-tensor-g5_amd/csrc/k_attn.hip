@@ -168,25 +168,36 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_kernel(AttnArgs a) {
     for (int t = 0; t < MTD; ++t) o[t] = floatx16{};
     float m_run = -INFINITY, l_run = 0.f;
 
+    // K / V tile loads: buffer loads whose per-thread byte offsets are fixed (tile key
+    // 0) and move by one add per tile; keys past Sk and threads without a chunk read
+    // past the resource's range and get zeros.  No branches, so all loads of a tile
+    // stay in flight while the current tile is computed.
     const f16* kbase = a.k + (int64_t)b * a.Sk * a.ldk + (int64_t)h * d;
     const f16* vbase = a.v + (int64_t)b * a.Sk * a.ldv + (int64_t)h * d;
+    const __amdgpu_buffer_rsrc_t rsk = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)kbase, (short)0, ((a.Sk - 1) * a.ldk + d) * 2, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsv = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)vbase, (short)0, ((a.Sk - 1) * a.ldv + d) * 2, 0x00020000);
     constexpr int MAXCH = (KT * KS * 2 + NTH - 1) / NTH;  // >= KT*d/8/NTH
     uint4 rk[MAXCH], rv[MAXCH];
     const int nchunk = KT * dch;
-
+    uint32_t kvo[MAXCH], vvo[MAXCH];
+    int sto[MAXCH];  // LDS position: key * KSTR + dc*8 (K); -1: no chunk
+#pragma unroll
+    for (int i = 0; i < MAXCH; ++i) {
+        const int cidx = tid + i * NTH;
+        const int key = cidx / dch, dc = cidx - key * dch;
+        const bool ok = cidx < nchunk;
+        kvo[i] = ok ? (uint32_t)((key * a.ldk + dc * 8) * 2) : 0x80000000u;
+        vvo[i] = ok ? (uint32_t)((key * a.ldv + dc * 8) * 2) : 0x80000000u;
+        sto[i] = ok ? key * 65536 + dc * 8 : -1;
+    }
     auto load_kv = [&](int kb) {
+        const uint32_t ko = (uint32_t)(kb * a.ldk * 2), vo = (uint32_t)(kb * a.ldv * 2);
 #pragma unroll
         for (int i = 0; i < MAXCH; ++i) {
-            const int cidx = tid + i * NTH;
-            uint4 kv = make_uint4(0, 0, 0, 0), vv = kv;
-            if (cidx < nchunk) {
-                const int key = cidx / dch, dc = cidx - key * dch;
-                const int j = kb + key;
-                if (j < a.Sk) {
-                    kv = *(const uint4*)(kbase + (int64_t)j * a.ldk + dc * 8);
-                    vv = *(const uint4*)(vbase + (int64_t)j * a.ldv + dc * 8);
-                }
-            }
+            const uint4 kv = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsk, kvo[i] + ko, 0, 0));
+            const uint4 vv = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsv, vvo[i] + vo, 0, 0));
             rk[i] = kv;
             rv[i] = vv;
         }
@@ -194,13 +205,12 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_kernel(AttnArgs a) {
     auto store_kv = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < MAXCH; ++i) {
-            const int cidx = tid + i * NTH;
-            if (cidx < nchunk) {
-                const int key = cidx / dch, dc = cidx - key * dch;
-                *(uint4*)&Ks[buf][key * KSTR + dc * 8] = rk[i];
+            if (sto[i] >= 0) {
+                const int key = sto[i] >> 16, c8 = sto[i] & 0xffff;
+                *(uint4*)&Ks[buf][key * KSTR + c8] = rk[i];
                 const f16* vh = (const f16*)&rv[i];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) Vt[buf][(dc * 8 + e) * VSTR + key] = vh[e];
+                for (int e = 0; e < 8; ++e) Vt[buf][(c8 + e) * VSTR + key] = vh[e];
             }
         }
     };
