@@ -98,6 +98,21 @@ int sdu_denoise_lcm_device(sdu_ctx* ctx, const float* d_lat, const float* d_cond
                            const float* d_uncond, int H, int W, int L, int steps,
                            float guidance, const float* d_noise, float* d_out);
 
+/* Device LCM denoise with the generation options of TpuUnetPipeline.kt:82-112
+ * (replaces its host loop over tpuForward / LcmScheduler.step):
+ *  - cfg_steps in [0, steps]: steps 0 .. cfg_steps-1 run the batch-CFG forward (B=2,
+ *    eps = u + guidance (c - u)); the later steps run one B=1 forward on cond and use
+ *    its eps directly (:94-99).  guidance <= 1 disables CFG on every step (:97).
+ *    cfg_steps = steps is sdu_denoise_lcm_device.
+ *  - d_noise: [steps-1,4,H,W] fp32 device noise, or NULL to draw it on the device:
+ *    element i = float(sqrt(-2 ln u1) cos(2 pi u2)) of the seeded generator with
+ *    key = fnv1a64("lcm.noise") ^ splitmix64(noise_seed) (:100 draws it from its own
+ *    RNG; the stream differs, the distribution is the same).
+ * Each (H, W, L, steps, guidance, cfg_steps) records its own HIP graph. */
+int sdu_denoise_lcm_ex(sdu_ctx* ctx, const float* d_lat, const float* d_cond,
+                       const float* d_uncond, int H, int W, int L, int steps, float guidance,
+                       int cfg_steps, const float* d_noise, uint64_t noise_seed, float* d_out);
+
 /* unetSelfTest (vk_engine.cpp:811-851): reads fixture_dir/IN_lat.bin (fp16 [4,64,64]),
  * IN_ctx.bin (fp16 [77,768]), IN_temb_proj.bin (fp16 [320]) and OUT_y.bin (fp16),
  * runs B=1 and B=2 (same input in both slots) and returns the largest

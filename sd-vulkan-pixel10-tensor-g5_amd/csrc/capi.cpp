@@ -171,8 +171,21 @@ int sdu_denoise_lcm_device(sdu_ctx* ctx, const float* d_lat, const float* d_cond
                            float* d_out) {
     SDU_GUARD(ctx);
     if (!d_lat || !d_cond || !d_uncond || !d_out) return fail(ctx, SDU_ERR_ARG, "null argument");
+    if (steps > 1 && !d_noise) return fail(ctx, SDU_ERR_ARG, "noise is required when steps > 1");
     return guarded(ctx, [&] {
-        return unet_denoise_device(ctx->c, d_lat, d_cond, d_uncond, H, W, L, steps, guidance, d_noise, d_out);
+        return unet_denoise_device(ctx->c, d_lat, d_cond, d_uncond, H, W, L, steps, guidance, steps, d_noise, 0,
+                                   d_out);
+    });
+}
+
+int sdu_denoise_lcm_ex(sdu_ctx* ctx, const float* d_lat, const float* d_cond, const float* d_uncond, int H,
+                       int W, int L, int steps, float guidance, int cfg_steps, const float* d_noise,
+                       uint64_t noise_seed, float* d_out) {
+    SDU_GUARD(ctx);
+    if (!d_lat || !d_cond || !d_uncond || !d_out) return fail(ctx, SDU_ERR_ARG, "null argument");
+    return guarded(ctx, [&] {
+        return unet_denoise_device(ctx->c, d_lat, d_cond, d_uncond, H, W, L, steps, guidance, cfg_steps, d_noise,
+                                   noise_seed, d_out);
     });
 }
 
@@ -196,7 +209,7 @@ int sdu_denoise_lcm(sdu_ctx* ctx, const float* lat, const float* cond, const flo
             (e = hipMemcpyAsync(du, uncond, cl * 4, hipMemcpyHostToDevice, s)) ||
             (nn && (e = hipMemcpyAsync(dn, noise, nn * 4, hipMemcpyHostToDevice, s))))
             st = hipfail(ctx, e, "upload");
-        if (!st) st = unet_denoise_device(ctx->c, dl, dc, du, H, W, L, steps, guidance, nn ? dn : nullptr, dout);
+        if (!st) st = unet_denoise_device(ctx->c, dl, dc, du, H, W, L, steps, guidance, steps, nn ? dn : nullptr, 0, dout);
         if (!st && ((e = hipMemcpyAsync(out, dout, n * 4, hipMemcpyDeviceToHost, s)) ||
                     (e = hipStreamSynchronize(s))))
             st = hipfail(ctx, e, "download");

@@ -133,8 +133,8 @@ int unet_forward_host(Ctx& c, const float* lat, const float* temb, const float* 
 int unet_forward_device(Ctx& c, const float* d_lat, const float* d_temb, const float* d_ctx, int B,
                         int H, int W, int L, float* d_out);
 int unet_denoise_device(Ctx& c, const float* d_lat, const float* d_cond, const float* d_uncond,
-                        int H, int W, int L, int steps, float guidance, const float* d_noise,
-                        float* d_out);
+                        int H, int W, int L, int steps, float guidance, int cfg_steps,
+                        const float* d_noise, uint64_t noise_seed, float* d_out);
 int unet_profile(Ctx& c, int B, int H, int W, int L);
 void free_fwd_states(Ctx& c);
 

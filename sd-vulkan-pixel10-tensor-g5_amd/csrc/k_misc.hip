@@ -117,8 +117,8 @@ __global__ void lcm_step_kernel(float* x, const float* eps2, const float* noise,
     // Every operation rounds separately (no FMA contraction), in the order of the
     // host formulas, so the device loop reproduces a host loop bit for bit.
     // eps = u + s (c - u) in float32 (VulkanUnetPipeline.kt:86)
-    const float ec = eps2[i], eu = eps2[n + i];
-    const float eps = __fadd_rn(eu, __fmul_rn(c.guidance, __fsub_rn(ec, eu)));
+    const float ec = eps2[i];
+    const float eps = c.cond_only ? ec : __fadd_rn(eps2[n + i], __fmul_rn(c.guidance, __fsub_rn(ec, eps2[n + i])));
     // LcmScheduler.kt:70-79 in float64
     const double xv = (double)x[i];
     const double x0 = __ddiv_rn(__dsub_rn(xv, __dmul_rn(c.sqrt_beta, (double)eps)), c.sqrt_alpha);
@@ -192,6 +192,26 @@ __global__ void gen_kernel(f16* dst, GenDesc g) {
     const double u2 = (double)(h2 >> 11) * 0x1.0p-53;
     const double z = sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
     dst[i] = f16_via_f32((float)__dadd_rn(g.mean, __dmul_rn(g.stdv, z)));
+}
+
+// fp32 N(0, 1) draws of the same generator (TpuUnetPipeline.kt:100 draws the per-step
+// noise as FloatArray(latSize) { gaussian(rnd) }): value = float(z).
+__global__ void gen_normal_f32_kernel(float* dst, int64_t n, uint64_t key) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint64_t h1 = mix64(key + 2ULL * (uint64_t)i);
+    const uint64_t h2 = mix64(key + 2ULL * (uint64_t)i + 1ULL);
+    const double u1 = (double)((h1 >> 11) + 1ULL) * 0x1.0p-53;
+    const double u2 = (double)(h2 >> 11) * 0x1.0p-53;
+    dst[i] = (float)(sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2));
+}
+
+hipError_t gen_normal_f32_launch(float* dst, int64_t n, uint64_t key, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    launch_timed("gen_normal_f32_kernel", 0.0, 4.0 * n, [&] {
+        hipLaunchKernelGGL(gen_normal_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, dst, n, key);
+    });
+    return hipGetLastError();
 }
 
 hipError_t gen_launch(f16* dst, const GenDesc& g, hipStream_t s) {

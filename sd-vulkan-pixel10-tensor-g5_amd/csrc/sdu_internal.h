@@ -132,6 +132,7 @@ struct LcmCoeffs {
     float guidance;
     double sqrt_alpha, sqrt_beta, c_skip, c_out, sqrt_alpha_prev, sqrt_beta_prev;
     int last;
+    int cond_only;  // eps = cond (a step without CFG: eps2 holds only the cond half)
 };
 // eps2: [2, n] (cond, uncond) fp32; x: [n] fp32 updated in place; noise [n] or null.
 // If unet_in != null, also writes the next UNet input NHWC fp16 [2, HW, Cpad]
@@ -152,6 +153,8 @@ struct GenDesc {
     int constant;      // 1: fill `mean` (no randomness)
 };
 hipError_t gen_launch(f16* dst, const GenDesc& g, hipStream_t s);
+// n fp32 N(0,1) values of the same generator (element i from key, no fp16 rounding).
+hipError_t gen_normal_f32_launch(float* dst, int64_t n, uint64_t key, hipStream_t s);
 
 uint64_t fnv1a64(const char* s);
 uint64_t splitmix64(uint64_t x);

@@ -468,6 +468,7 @@ struct FwdState {
     Fwd f;
     int steps = 0;
     float guidance = 0.f;
+    int cfg_steps = 0;  // denoise: steps [0, cfg_steps) run batch CFG, the rest cond only
     char* arena = nullptr;
     size_t arena_bytes = 0;
     float* gemm_ws = nullptr;
@@ -505,8 +506,16 @@ static void body(Exec& E, FwdState& S) {
     const f16* kv = cross_kv(E, ctx16, F.L);  // context is fixed across steps
     LcmSched sched(S.steps);
     for (int i = 0; i < S.steps; ++i) {
-        unet_core(E, F, lat, S.in_temb + (size_t)i * 320, kv, eps2);
-        const LcmCoeffs co = sched.coeffs(i, S.guidance);
+        // TpuUnetPipeline.kt:94-99: CFG on the first cfg_steps steps, then one forward on
+        // cond alone (its image 0: slot 0 of the input, the first L rows of K/V)
+        const bool cfg = S.guidance > 1.f && i < S.cfg_steps;
+        E.B = cfg ? 2 : 1;
+        Fwd Fi = F;
+        Fi.B = E.B;
+        unet_core(E, Fi, lat, S.in_temb + (size_t)i * 320, kv, eps2);
+        E.B = 2;
+        LcmCoeffs co = sched.coeffs(i, S.guidance);
+        co.cond_only = !cfg;
         const float* nz = co.last ? nullptr : S.in_noise + (size_t)i * n;
         f16* next = co.last ? nullptr : lat;
         E.run("lcm_step", [&] {
@@ -587,16 +596,18 @@ static int plan_state(Ctx& c, FwdState& S) {
     return SDU_OK;
 }
 
-static FwdState* get_state(Ctx& c, int kind, int B, int H, int W, int L, int steps, float guidance, int* st) {
+static FwdState* get_state(Ctx& c, int kind, int B, int H, int W, int L, int steps, float guidance,
+                           int cfg_steps, int* st) {
     for (FwdState* s : c.fwd)
         if (s->kind == kind && s->f.B == B && s->f.H == H && s->f.W == W && s->f.L == L &&
-            s->steps == steps && (kind == 0 || s->guidance == guidance))
+            s->steps == steps && (kind == 0 || (s->guidance == guidance && s->cfg_steps == cfg_steps)))
             return s;
     std::unique_ptr<FwdState> S(new FwdState());
     S->kind = kind;
     S->f = Fwd{B, H, W, L};
     S->steps = steps;
     S->guidance = guidance;
+    S->cfg_steps = cfg_steps;
     *st = plan_state(c, *S);
     if (*st) { free_state(S.get()); return nullptr; }
     c.fwd.push_back(S.release());
@@ -614,7 +625,7 @@ int unet_forward_device(Ctx& c, const float* d_lat, const float* d_temb, const f
                         int W, int L, float* d_out) {
     int st = check_shape(c, B, H, W, L);
     if (st) return st;
-    FwdState* S = get_state(c, 0, B, H, W, L, 0, 0.f, &st);
+    FwdState* S = get_state(c, 0, B, H, W, L, 0, 0.f, 0, &st);
     if (!S) return st;
     const size_t lat_b = (size_t)B * kLatC * H * W * 4;
     hipError_t e;
@@ -631,7 +642,7 @@ int unet_forward_host(Ctx& c, const float* lat, const float* temb, const float* 
                       int L, float* out) {
     int st = check_shape(c, B, H, W, L);
     if (st) return st;
-    FwdState* S = get_state(c, 0, B, H, W, L, 0, 0.f, &st);
+    FwdState* S = get_state(c, 0, B, H, W, L, 0, 0.f, 0, &st);
     if (!S) return st;
     const size_t lat_b = (size_t)B * kLatC * H * W * 4;
     hipError_t e;
@@ -646,12 +657,14 @@ int unet_forward_host(Ctx& c, const float* lat, const float* temb, const float* 
 }
 
 int unet_denoise_device(Ctx& c, const float* d_lat, const float* d_cond, const float* d_uncond, int H,
-                        int W, int L, int steps, float guidance, const float* d_noise, float* d_out) {
+                        int W, int L, int steps, float guidance, int cfg_steps, const float* d_noise,
+                        uint64_t noise_seed, float* d_out) {
     int st = check_shape(c, 2, H, W, L);
     if (st) return st;
     if (steps < 1 || steps > 50) return set_err(&c, SDU_ERR_ARG, "steps must be in 1..50");
-    if (steps > 1 && !d_noise) return set_err(&c, SDU_ERR_ARG, "noise is required when steps > 1");
-    FwdState* S = get_state(c, 1, 2, H, W, L, steps, guidance, &st);
+    if (cfg_steps < 0 || cfg_steps > steps) return set_err(&c, SDU_ERR_ARG, "cfg_steps must be in 0..steps");
+    if (!(guidance > 1.f)) cfg_steps = 0;  // no CFG on any step (TpuUnetPipeline.kt:97)
+    FwdState* S = get_state(c, 1, 2, H, W, L, steps, guidance, cfg_steps, &st);
     if (!S) return st;
     const size_t n = (size_t)kLatC * H * W;
     const size_t cb = (size_t)L * kCtxDim * 4;
@@ -660,9 +673,14 @@ int unet_denoise_device(Ctx& c, const float* d_lat, const float* d_cond, const f
         (e = hipMemcpyAsync(S->in_ctx, d_cond, cb, hipMemcpyDeviceToDevice, c.stream)) ||
         (e = hipMemcpyAsync((char*)S->in_ctx + cb, d_uncond, cb, hipMemcpyDeviceToDevice, c.stream)))
         return hip_fail(c, e, "denoise");
-    if (steps > 1 && (e = hipMemcpyAsync(S->in_noise, d_noise, (size_t)(steps - 1) * n * 4,
-                                         hipMemcpyDeviceToDevice, c.stream)))
-        return hip_fail(c, e, "denoise");
+    if (steps > 1) {
+        // caller's noise, or N(0,1) drawn on the device from noise_seed
+        e = d_noise ? hipMemcpyAsync(S->in_noise, d_noise, (size_t)(steps - 1) * n * 4, hipMemcpyDeviceToDevice,
+                                     c.stream)
+                    : gen_normal_f32_launch(S->in_noise, (int64_t)(steps - 1) * n,
+                                            fnv1a64("lcm.noise") ^ splitmix64(noise_seed), c.stream);
+        if (e != hipSuccess) return hip_fail(c, e, "denoise");
+    }
     if ((e = hipGraphLaunch(S->exec, c.stream)) ||
         (e = hipMemcpyAsync(d_out, S->out, n * 4, hipMemcpyDeviceToDevice, c.stream)))
         return hip_fail(c, e, "denoise");
@@ -677,7 +695,7 @@ int unet_denoise_device(Ctx& c, const float* d_lat, const float* d_cond, const f
 int unet_profile(Ctx& c, int B, int H, int W, int L) {
     int st = check_shape(c, B, H, W, L);
     if (st) return st;
-    FwdState* S = get_state(c, 0, B, H, W, L, 0, 0.f, &st);
+    FwdState* S = get_state(c, 0, B, H, W, L, 0, 0.f, 0, &st);
     if (!S) return st;
     hipError_t e = hipStreamSynchronize(c.stream);
     if (e != hipSuccess) return hip_fail(c, e, "profile");

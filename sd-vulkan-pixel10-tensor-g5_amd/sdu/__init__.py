@@ -36,7 +36,7 @@ SDU_EPI_OUT_F32 = 0x2
 EXPORTS = [
     "sdu_init", "sdu_release", "sdu_last_error", "sdu_synchronize", "sdu_set_weight",
     "sdu_get_weight", "sdu_param_count", "sdu_forward", "sdu_forward_cfg", "sdu_denoise_lcm",
-    "sdu_forward_device", "sdu_denoise_lcm_device", "sdu_selftest", "sdu_profile",
+    "sdu_forward_device", "sdu_denoise_lcm_device", "sdu_denoise_lcm_ex", "sdu_selftest", "sdu_profile",
     "sdu_tensor_alloc", "sdu_tensor_free", "sdu_tensor_upload", "sdu_tensor_download",
     "sdu_tensor_device_ptr", "sdu_tensor_bytes", "sdu_groupnorm", "sdu_layernorm", "sdu_matmul",
     "sdu_conv2d", "sdu_attention", "sdu_geglu", "sdu_silu", "sdu_add", "sdu_add_bias",
@@ -86,6 +86,7 @@ def load(path: str = LIB_PATH):
         "sdu_denoise_lcm": ([P, P, P, P, I, I, I, I, F, P, P], I),
         "sdu_forward_device": ([P, P, P, P, I, I, I, I, P], I),
         "sdu_denoise_lcm_device": ([P, P, P, P, I, I, I, I, F, P, P], I),
+        "sdu_denoise_lcm_ex": ([P, P, P, P, I, I, I, I, F, I, P, ctypes.c_uint64, P], I),
         "sdu_selftest": ([P, ctypes.c_char_p], ctypes.c_double),
         "sdu_profile": ([P, I, I, I, I, P, I, ctypes.POINTER(I), ctypes.POINTER(ctypes.c_double)], I),
         "sdu_tensor_alloc": ([P, I, I, ctypes.POINTER(I64), ctypes.POINTER(P)], I),
@@ -243,6 +244,12 @@ class Engine:
     def denoise_lcm_device(self, d_lat, d_cond, d_uncond, H, W, L, steps, guidance, d_noise, d_out):
         self._check(load().sdu_denoise_lcm_device(self.h, d_lat, d_cond, d_uncond, H, W, L, steps,
                                                   guidance, d_noise, d_out))
+
+    def denoise_lcm_ex(self, d_lat, d_cond, d_uncond, H, W, L, steps, guidance, cfg_steps, d_noise,
+                       noise_seed, d_out):
+        """d_noise may be None: the noise is then drawn on the device from noise_seed."""
+        self._check(load().sdu_denoise_lcm_ex(self.h, d_lat, d_cond, d_uncond, H, W, L, steps, guidance,
+                                              cfg_steps, d_noise, noise_seed, d_out))
 
     def selftest(self, fixture_dir: str) -> float:
         return float(load().sdu_selftest(self.h, fixture_dir.encode()))

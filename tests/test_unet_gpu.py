@@ -158,6 +158,67 @@ def test_denoise_loop_matches_host_loop(unet_engine):
     assert np.array_equal(dev, x)
 
 
+def _denoise_ex(eng, lat, cond, unc, steps, g, cfg_steps, noise, seed=0):
+    import sdu
+    H, W = lat.shape[1:]
+    d = [eng.upload(a) for a in (lat, cond, unc)]
+    dn = eng.upload(noise) if noise is not None else None
+    out = eng.tensor((4, H, W), sdu.SDU_F32)
+    eng.denoise_lcm_ex(d[0].ptr, d[1].ptr, d[2].ptr, H, W, cond.shape[0], steps, g, cfg_steps,
+                       dn.ptr if dn is not None else None, seed, out.ptr)
+    return out.numpy()
+
+
+def test_denoise_cfg_first_steps(unet_engine):
+    """CFG on the first cfg_steps steps only (TpuUnetPipeline.kt:94-99): the device
+    loop against a host loop of the engine's own forwards -- batch CFG for the first
+    two steps, then B=1 on cond with eps used as is -- and the oracle's float64 step.
+    The B=1 steps of the device loop take cond's K/V rows from the B=2 cross-K/V GEMM,
+    whose tile plan differs from a B=1 forward's, so the bar is relErr, not equality."""
+    steps, g, H, W, k = 4, 8.0, 32, 32, 2
+    lat, cond, unc, noise = _denoise_inputs(H, W, steps)
+    say(f"denoise LCM cfg_steps={k}")
+    dev = _denoise_ex(unet_engine, lat, cond, unc, steps, g, k, noise)
+    sched = lcm.LcmSchedule(steps)
+    x = lat.copy()
+    for idx, t in enumerate(sched.timesteps):
+        if idx < k:
+            both = unet_engine.forward_cfg(x, lcm.time_proj(t), cond, unc)
+            eps = lcm.cfg_combine(both[0], both[1], g)
+        else:
+            eps = unet_engine.forward(x[None], lcm.time_proj(t), cond[None])[0]
+        x = sched.step(idx, x, eps, None if idx == steps - 1 else noise[idx])
+    e = rel_err_l1(dev, x)
+    say(f"  relErr vs host loop {e:.2e}")
+    assert e <= 1e-3
+    # cfg_steps = steps is the batch-CFG loop
+    full = _denoise_ex(unet_engine, lat, cond, unc, steps, g, steps, noise)
+    assert np.array_equal(full, unet_engine.denoise_lcm(lat, cond, unc, steps, g, noise))
+    # guidance <= 1 disables CFG on every step: the same as cfg_steps = 0
+    a = _denoise_ex(unet_engine, lat, cond, unc, steps, 1.0, steps, noise)
+    b = _denoise_ex(unet_engine, lat, cond, unc, steps, g, 0, noise)
+    assert np.array_equal(a, b)
+    assert rel_err_l1(a, full) > 1e-2  # and it is a different result
+
+
+def test_denoise_device_noise(unet_engine):
+    """noise = NULL draws N(0,1) on the device from the seed (key
+    fnv1a64("lcm.noise") ^ splitmix64(seed)); the oracle's generator with the same key
+    gives the same noise, so the two runs agree."""
+    steps, g, H, W = 4, 8.0, 32, 32
+    lat, cond, unc, _ = _denoise_inputs(H, W, steps)
+    seed = 77
+    noise = Wt.gauss("lcm.noise", (steps - 1, 4, H, W), seed, fp16=False)
+    assert abs(float(noise.mean())) < 0.05 and abs(float(noise.std()) - 1.0) < 0.05
+    a = _denoise_ex(unet_engine, lat, cond, unc, steps, g, steps, None, seed)
+    b = _denoise_ex(unet_engine, lat, cond, unc, steps, g, steps, noise)
+    e = rel_err_l1(a, b)
+    say(f"device noise vs oracle noise: relErr {e:.2e}")
+    assert e <= 1e-6
+    c = _denoise_ex(unet_engine, lat, cond, unc, steps, g, steps, None, seed + 1)
+    assert rel_err_l1(a, c) > 1e-3
+
+
 def _denoise_case(unet_engine, oracle_weights, H, W):
     """4-step LCM + CFG (guidance 8) vs the oracle loop with the same injected
     noise (VulkanUnetPipeline.kt:63-97, LcmScheduler.kt:56-82).
