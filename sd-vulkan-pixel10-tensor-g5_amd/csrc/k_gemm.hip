@@ -650,15 +650,17 @@ struct Cfg {
     double t_fix;         // per-block prologue + epilogue time
 };
 // 0: 256x128, 8 waves of 64x64, BK 64, 2-stage ring (96 KB: one block per CU)
-// 1: 128x128, 4 waves of 64x64, BK 64, 2-stage ring (64 KB: two per CU)
-// 2: 128x64,  4 waves of 64x32, BK 64, 3-stage ring (72 KB: two per CU)
-const Cfg kCfgs[3] = {{256, 128, 1, 3.3e12, 3.3e12, 4.5e-6},
-                      {128, 128, 2, 2.4e12, 3.4e12, 3.0e-6},
-                      {128, 64, 2, 1.6e12, 2.4e12, 2.5e-6}};
+// 1: 128x128, 8 waves of 64x32, BK 64, 2-stage ring (64 KB: two per CU, 4 waves per SIMD)
+// 2: 128x64,  8 waves of 32x32, BK 64, 3-stage ring (72 KB: two per CU, 4 waves per SIMD)
+// Rates and fixed costs from dense GEMMs that give every CU one or two blocks, at
+// K = 512 and 4096 (the difference gives the rate, the rest the fixed cost).
+const Cfg kCfgs[3] = {{256, 128, 1, 3.5e12, 3.5e12, 4.5e-6},
+                      {128, 128, 2, 2.76e12, 3.54e12, 3.0e-6},
+                      {128, 64, 2, 2.23e12, 3.03e12, 2.5e-6}};
 // full kernel names (tile configuration, then the A mode: 0 dense, 1 implicit conv)
 const char* const kNames[3][2] = {{"gemm_kernel<256,128,4,2,64,2,0>", "gemm_kernel<256,128,4,2,64,2,1>"},
-                                  {"gemm_kernel<128,128,2,2,64,2,0>", "gemm_kernel<128,128,2,2,64,2,1>"},
-                                  {"gemm_kernel<128,64,2,2,64,3,0>", "gemm_kernel<128,64,2,2,64,3,1>"}};
+                                  {"gemm_kernel<128,128,2,4,64,2,0>", "gemm_kernel<128,128,2,4,64,2,1>"},
+                                  {"gemm_kernel<128,64,4,2,64,3,0>", "gemm_kernel<128,64,4,2,64,3,1>"}};
 
 int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
@@ -690,7 +692,8 @@ void plan(const GemmArgs& a, int& ci, int& splits, int& kps) {
             const double w = 2.0 * g.mt * g.nt * kt_per * 64.0;
             const long pairs = g.per_cu >= 2 ? load / 2 : 0, singles = load - 2 * pairs;
             double t = pairs * (2.0 * w / g.rate2 + g.t_fix) + singles * (w / g.rate1 + g.t_fix);
-            if (se > 1) t += (double)se * a.M * a.N * 8.0 / 20.0e12 + 4.0e-6;
+            // the reduce launch: about 5.5 us plus its traffic (2 us more with statistics)
+            if (se > 1) t += (double)se * a.M * a.N * 8.0 / 20.0e12 + (a.stats ? 7.5e-6 : 5.5e-6);
             if (t < best * 0.98) { best = t; ci = c; splits = se; kps = kt_per * 64; }
         }
     }
@@ -714,8 +717,8 @@ size_t gemm_workspace_bytes(const GemmArgs& a) {
 template <int AM>
 static void launch_cfg(int ci, dim3 grid, const GemmArgs& a, hipStream_t s) {
     if (ci == 0) hipLaunchKernelGGL((gemm_kernel<256, 128, 4, 2, 64, 2, AM>), grid, dim3(512), 0, s, a);
-    else if (ci == 1) hipLaunchKernelGGL((gemm_kernel<128, 128, 2, 2, 64, 2, AM>), grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((gemm_kernel<128, 64, 2, 2, 64, 3, AM>), grid, dim3(256), 0, s, a);
+    else if (ci == 1) hipLaunchKernelGGL((gemm_kernel<128, 128, 2, 4, 64, 2, AM>), grid, dim3(512), 0, s, a);
+    else hipLaunchKernelGGL((gemm_kernel<128, 64, 4, 2, 64, 3, AM>), grid, dim3(512), 0, s, a);
 }
 
 hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s) {
