@@ -416,8 +416,10 @@ static void launch_cfg(const AttnArgs& a, hipStream_t s) {
     const double flops = 4.0 * bh * a.Sq * a.Sk * a.d;
     const double bytes = 2.0 * bh * a.d * (2.0 * a.Sq + 2.0 * a.Sk);
     char name[48];
-    if (qwaves >= 1024) {
-        // shared K/V tiles; two waves per block when four would leave < 512 blocks
+    // shared K/V tiles where there are enough query waves, or half as many with long
+    // key sequences (the key-split kernel re-reads K/V per wave); two waves per block
+    // when four would leave < 512 blocks
+    if (qwaves >= 1024 || (qwaves >= 512 && a.Sk >= 512)) {
         const int nw = ((a.Sq + 127) / 128) * bh >= 512 ? 4 : 2;
         snprintf(name, sizeof name, "attn_kernel<%d,%d,%d,%d>", KS, MTD, nw, (int)LSUM);
         const dim3 grid((a.Sq + nw * 32 - 1) / (nw * 32), a.heads, a.B);

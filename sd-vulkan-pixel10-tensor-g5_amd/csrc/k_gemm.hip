@@ -200,8 +200,8 @@ __device__ __forceinline__ void reduce_rows(const GemmArgs& a, const int (&m)[R]
 
 // Split-K reduce for outputs whose channel statistics are needed: block = 8 column
 // chunks (64 columns) x 32 row phases, each thread SR rows (rows of a block:
-// 32 * SR = 64 <= stats_hw, so a block spans at most two images).
-static constexpr int SR = 2;
+// 32 * SR <= 64 <= stats_hw, so a block spans at most two images).
+template <int SR>
 __global__ __launch_bounds__(256) void splitk_reduce_stats_kernel(GemmArgs a) {
     const int tid = threadIdx.x;
     const int col0 = blockIdx.x * 64;
@@ -691,7 +691,10 @@ void plan(const GemmArgs& a, int& ci, int& splits, int& kps) {
             const long load = (blocks + 255) / 256;  // blocks on the busiest CU
             const double w = 2.0 * g.mt * g.nt * kt_per * 64.0;
             const long pairs = g.per_cu >= 2 ? load / 2 : 0, singles = load - 2 * pairs;
-            double t = pairs * (2.0 * w / g.rate2 + g.t_fix) + singles * (w / g.rate1 + g.t_fix);
+            // implicit-conv A (a tap gather per 128 rows) costs the 64-column tile a
+            // larger share of its time than a dense A: about 20% of its rate
+            const double cf = (a.amode == A_CONV3 && g.nt < 128) ? 0.8 : 1.0;
+            double t = pairs * (2.0 * w / (g.rate2 * cf) + g.t_fix) + singles * (w / (g.rate1 * cf) + g.t_fix);
             // the reduce launch: about 5.5 us plus its traffic (2 us more with statistics)
             if (se > 1) t += (double)se * a.M * a.N * 8.0 / 20.0e12 + (a.stats ? 7.5e-6 : 5.5e-6);
             if (t < best * 0.98) { best = t; ci = c; splits = se; kps = kt_per * 64; }
@@ -758,9 +761,13 @@ hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s) {
     const bool vec = a.out_mode != OUT_F32_NCHW && (a.N & 7) == 0;
     const int64_t total = (int64_t)a.M * (vec ? nout / 8 : nout);
     if (a.stats) {
-        const dim3 grid((unsigned)ceil_div(a.N, 64), (unsigned)ceil_div(a.M, 32 * SR));
-        launch_timed("splitk_reduce_stats_kernel", 0.0, part_bytes + out_bytes, [&] {
-            hipLaunchKernelGGL(splitk_reduce_stats_kernel, grid, dim3(256), 0, s, a);
+        // two rows per thread when that still gives every CU a block
+        const bool two = (long)ceil_div(a.N, 64) * ceil_div(a.M, 64) >= 256;
+        const dim3 grid((unsigned)ceil_div(a.N, 64), (unsigned)ceil_div(a.M, two ? 64 : 32));
+        launch_timed(two ? "splitk_reduce_stats_kernel<2>" : "splitk_reduce_stats_kernel<1>", 0.0,
+                     part_bytes + out_bytes, [&] {
+            if (two) hipLaunchKernelGGL(splitk_reduce_stats_kernel<2>, grid, dim3(256), 0, s, a);
+            else hipLaunchKernelGGL(splitk_reduce_stats_kernel<1>, grid, dim3(256), 0, s, a);
         });
     } else {
         launch_timed("splitk_reduce_kernel", 0.0, part_bytes + out_bytes, [&] {
