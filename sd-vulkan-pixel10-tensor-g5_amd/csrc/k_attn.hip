@@ -178,39 +178,68 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_kernel(AttnArgs a) {
         (void*)kbase, (short)0, ((a.Sk - 1) * a.ldk + d) * 2, 0x00020000);
     const __amdgpu_buffer_rsrc_t rsv = __builtin_amdgcn_make_buffer_rsrc(
         (void*)vbase, (short)0, ((a.Sk - 1) * a.ldv + d) * 2, 0x00020000);
-    constexpr int MAXCH = (KT * KS * 2 + NTH - 1) / NTH;  // >= KT*d/8/NTH
-    uint4 rk[MAXCH], rv[MAXCH];
-    const int nchunk = KT * dch;
-    uint32_t kvo[MAXCH], vvo[MAXCH];
-    int sto[MAXCH];  // LDS position: key * KSTR + dc*8 (K); -1: no chunk
+    // K: one 16-byte chunk (8 dims of one key) per thread and step, stored as is.
+    // V: one unit = the same 8 dims of 4 consecutive keys per thread and step, so that
+    // the transposed store to V^T [dim][key] is 8 ds_write_b64 (4 keys of one dim each)
+    // instead of 32 two-byte stores.
+    constexpr int MAXCH = (KT * KS * 2 + NTH - 1) / NTH;        // >= KT*d/8/NTH
+    constexpr int MAXU = (KT / 4 * KS * 2 + NTH - 1) / NTH;     // >= (KT/4)*(d/8)/NTH
+    uint4 rk[MAXCH], rv[MAXU][4];
+    const int nchunk = KT * dch, nunit = KT / 4 * dch;
+    uint32_t kvo[MAXCH], vvo[MAXU];
+    int sto[MAXCH];  // LDS position of the K chunk: key << 16 | dc*8; -1: no chunk
+    int vto[MAXU];   // V unit: first key << 16 | dc*8; -1: no unit
 #pragma unroll
     for (int i = 0; i < MAXCH; ++i) {
         const int cidx = tid + i * NTH;
         const int key = cidx / dch, dc = cidx - key * dch;
         const bool ok = cidx < nchunk;
         kvo[i] = ok ? (uint32_t)((key * a.ldk + dc * 8) * 2) : 0x80000000u;
-        vvo[i] = ok ? (uint32_t)((key * a.ldv + dc * 8) * 2) : 0x80000000u;
         sto[i] = ok ? key * 65536 + dc * 8 : -1;
+    }
+#pragma unroll
+    for (int i = 0; i < MAXU; ++i) {
+        const int u = tid + i * NTH;
+        const int kq = u / dch, dc = u - kq * dch;
+        const bool ok = u < nunit;
+        vvo[i] = ok ? (uint32_t)((4 * kq * a.ldv + dc * 8) * 2) : 0x80000000u;
+        vto[i] = ok ? 4 * kq * 65536 + dc * 8 : -1;
     }
     auto load_kv = [&](int kb) {
         const uint32_t ko = (uint32_t)(kb * a.ldk * 2), vo = (uint32_t)(kb * a.ldv * 2);
+        const uint32_t vrow = (uint32_t)(a.ldv * 2);
 #pragma unroll
-        for (int i = 0; i < MAXCH; ++i) {
-            const uint4 kv = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsk, kvo[i] + ko, 0, 0));
-            const uint4 vv = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsv, vvo[i] + vo, 0, 0));
-            rk[i] = kv;
-            rv[i] = vv;
-        }
+        for (int i = 0; i < MAXCH; ++i)
+            rk[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsk, kvo[i] + ko, 0, 0));
+#pragma unroll
+        for (int i = 0; i < MAXU; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                rv[i][j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                         rsv, vvo[i] + vo + j * vrow, 0, 0));
     };
     auto store_kv = [&](int buf) {
 #pragma unroll
-        for (int i = 0; i < MAXCH; ++i) {
-            if (sto[i] >= 0) {
-                const int key = sto[i] >> 16, c8 = sto[i] & 0xffff;
-                *(uint4*)&Ks[buf][key * KSTR + c8] = rk[i];
-                const f16* vh = (const f16*)&rv[i];
+        for (int i = 0; i < MAXCH; ++i)
+            if (sto[i] >= 0) *(uint4*)&Ks[buf][(sto[i] >> 16) * KSTR + (sto[i] & 0xffff)] = rk[i];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) Vt[buf][(c8 + e) * VSTR + key] = vh[e];
+        for (int i = 0; i < MAXU; ++i) {
+            if (vto[i] >= 0) {
+                const int key = vto[i] >> 16, c8 = vto[i] & 0xffff;
+                const uint32_t* w0 = (const uint32_t*)&rv[i][0];
+                const uint32_t* w1 = (const uint32_t*)&rv[i][1];
+                const uint32_t* w2 = (const uint32_t*)&rv[i][2];
+                const uint32_t* w3 = (const uint32_t*)&rv[i][3];
+#pragma unroll
+                for (int e2 = 0; e2 < 4; ++e2) {
+                    // dims 2*e2 (low halves) and 2*e2+1 (high halves) of the 4 keys
+                    const uint32_t lo01 = __builtin_amdgcn_perm(w1[e2], w0[e2], 0x05040100u);
+                    const uint32_t lo23 = __builtin_amdgcn_perm(w3[e2], w2[e2], 0x05040100u);
+                    const uint32_t hi01 = __builtin_amdgcn_perm(w1[e2], w0[e2], 0x07060302u);
+                    const uint32_t hi23 = __builtin_amdgcn_perm(w3[e2], w2[e2], 0x07060302u);
+                    *(uint2*)&Vt[buf][(c8 + 2 * e2) * VSTR + key] = make_uint2(lo01, lo23);
+                    *(uint2*)&Vt[buf][(c8 + 2 * e2 + 1) * VSTR + key] = make_uint2(hi01, hi23);
+                }
             }
         }
     };

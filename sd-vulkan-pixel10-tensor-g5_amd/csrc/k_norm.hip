@@ -203,9 +203,10 @@ __global__ __launch_bounds__(GN_THREADS) void gn_apply_kernel(const f16* x, cons
         const f16* hg = (const f16*)&gv[j];
         const f16* hb = (const f16*)&bv[j];
         float sc[8], sh[8];
+        int g = o * 8 / cpg, nb = (g + 1) * cpg;  // group of channel o*8, its end
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const int g = (o * 8 + e) / cpg;
+            if (o * 8 + e >= nb) { ++g; nb += cpg; }  // channels step by one: one group at a time
             sc[e] = s_rstd[g] * (float)hg[e];
             sh[e] = (float)hb[e] - s_mean[g] * sc[e];
         }
