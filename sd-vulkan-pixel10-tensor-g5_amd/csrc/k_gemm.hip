@@ -781,37 +781,60 @@ hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s) {
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }
 
-// One wave per output row; fp32 input vector, fp16 weights [N, K], K % 8 == 0.
+// y[n] = act_out(sum_k act_in(x[k]) W[n][k] + bias[n]).  act_in(x) is formed once per
+// block in LDS; each wave then takes GV_ROWS rows, lane l the 8-column chunks l, l+64,
+// ..., with all of a chunk's row loads issued together.  K % 8 == 0, K <= GV_MAXK.
+static constexpr int GV_ROWS = 4;
+static constexpr int GV_MAXK = 2048;
 __global__ __launch_bounds__(256) void gemv_kernel(const float* x, const f16* W, const f16* bias,
                                                    float* y, int N, int K, int act_in, int act_out) {
+    __shared__ __attribute__((aligned(16))) float xs[GV_MAXK];
+    for (int k = threadIdx.x; k < K; k += 256) {
+        const float v = x[k];
+        xs[k] = act_in ? silu_f(v) : v;
+    }
+    __syncthreads();
     const int lane = threadIdx.x & 63;
-    const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (n >= N) return;
-    float s = 0.f;
-    for (int k = lane * 8; k < K; k += 64 * 8) {
-        uint4 wv = *(const uint4*)(W + (int64_t)n * K + k);
-        const f16* wh = (const f16*)&wv;
+    const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * GV_ROWS;
+    float s[GV_ROWS];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            float xv = x[k + i];
-            if (act_in) xv = silu_f(xv);
-            s += xv * (float)wh[i];
+    for (int r = 0; r < GV_ROWS; ++r) s[r] = 0.f;
+#pragma unroll
+    for (int j = 0; j < GV_MAXK / 512; ++j) {
+        const int k = (lane + 64 * j) * 8;
+        if (k >= K) break;
+        uint4 wv[GV_ROWS];
+#pragma unroll
+        for (int r = 0; r < GV_ROWS; ++r) wv[r] = *(const uint4*)(W + (int64_t)min(row0 + r, N - 1) * K + k);
+        const float4 x0 = *(const float4*)&xs[k], x1 = *(const float4*)&xs[k + 4];
+        const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+        for (int r = 0; r < GV_ROWS; ++r) {
+            const f16* wh = (const f16*)&wv[r];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) s[r] += xv[i] * (float)wh[i];
         }
     }
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
-    if (lane == 0) {
-        if (bias) s += (float)bias[n];
-        if (act_out) s = silu_f(s);
-        y[n] = s;
+    for (int r = 0; r < GV_ROWS; ++r) {
+        float t = s[r];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) t += __shfl_xor(t, off);
+        const int n = row0 + r;
+        if (lane == 0 && n < N) {
+            if (bias) t += (float)bias[n];
+            if (act_out) t = silu_f(t);
+            y[n] = t;
+        }
     }
 }
 
 hipError_t gemv_launch(const float* x, const f16* W, const f16* bias, float* y, int N, int K,
                        int act_in, int act_out, hipStream_t s) {
+    if (N <= 0 || K <= 0 || K % 8 || K > GV_MAXK) return hipErrorInvalidValue;
     launch_timed("gemv_kernel", 2.0 * N * K, 2.0 * N * K + 4.0 * (N + K), [&] {
-        hipLaunchKernelGGL(gemv_kernel, dim3((N + 3) / 4), dim3(256), 0, s, x, W, bias, y, N, K, act_in,
-                           act_out);
+        hipLaunchKernelGGL(gemv_kernel, dim3((N + 4 * GV_ROWS - 1) / (4 * GV_ROWS)), dim3(256), 0, s, x, W, bias, y,
+                           N, K, act_in, act_out);
     });
     return hipGetLastError();
 }
