@@ -48,6 +48,17 @@ int finish(sdu_ctx* ctx, hipError_t e, const char* what) {
     return SDU_OK;
 }
 
+// An op-level GEMM on the context's scratch.  Other ops reuse that scratch, so the
+// split-K tile counters at its head are cleared before a split launch.
+int op_gemm(sdu_ctx* ctx, const GemmArgs& g, const char* what) {
+    const size_t ws = gemm_workspace_bytes(g);
+    const int st = ensure_op_ws(ctx->c, ws + 256);
+    if (st) return st;
+    hipError_t e = ws ? zero_launch(ctx->c.op_ws, gemm_counter_bytes(), ctx->c.stream) : hipSuccess;
+    if (e == hipSuccess) e = gemm_launch(g, ctx->c.op_ws, ctx->c.stream);
+    return finish(ctx, e, what);
+}
+
 }  // namespace
 
 extern "C" {
@@ -406,9 +417,7 @@ int sdu_matmul(sdu_ctx* ctx, const sdu_tensor* a, const sdu_tensor* a2, const sd
     g.C = dptr(y); g.ldc = Nout;
     g.out_mode = f32 ? OUT_F32 : OUT_F16;
     g.geglu = geglu;
-    int st = ensure_op_ws(ctx->c, gemm_workspace_bytes(g) + 256);
-    if (st) return st;
-    return finish(ctx, gemm_launch(g, ctx->c.op_ws, ctx->c.stream), "matmul");
+    return op_gemm(ctx, g, "matmul");
 }
 
 int sdu_conv2d(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* w, const sdu_tensor* bias,
@@ -447,9 +456,7 @@ int sdu_conv2d(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* w, const sdu
     g.res = (const f16*)dptr(residual); g.ldr = Co;
     g.C = dptr(y); g.ldc = Co;
     g.out_mode = f32 ? OUT_F32 : OUT_F16;
-    int st = ensure_op_ws(ctx->c, gemm_workspace_bytes(g) + 256);
-    if (st) return st;
-    return finish(ctx, gemm_launch(g, ctx->c.op_ws, ctx->c.stream), "conv2d");
+    return op_gemm(ctx, g, "conv2d");
 }
 
 int sdu_attention(sdu_ctx* ctx, const sdu_tensor* q, const sdu_tensor* k, const sdu_tensor* v,

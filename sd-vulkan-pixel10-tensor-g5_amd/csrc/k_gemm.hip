@@ -11,7 +11,8 @@
 // Epilogue (fused; the reference runs these as separate AB/AB2/ADD/GEGLU passes):
 // + bias[n] + bias2[n] (fp32 time projection), GEGLU over interleaved a/b column
 // blocks, + residual, store fp16 / fp32 / fp32-NCHW.
-// Split-K writes fp32 partial tiles; a reduce kernel applies the epilogue.
+// Split-K, two ways: the last block of a tile to arrive sums the tile's fp32 partials
+// and runs the epilogue (few splits), or a reduce kernel does (many splits).
 #include "sdu_internal.h"
 
 #include <algorithm>
@@ -20,6 +21,7 @@ namespace sdu {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float gelu_erf(float x) {
     return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));
@@ -499,7 +501,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
 
     // ---- epilogue
     const int col_l = lane & 31, rq = (lane >> 5) * 4;
-    if (a.partial) {
+    if (a.partial && !a.fixup) {
+        // split K, reduce kernel: fp32 partial [split][M][N]
         float* P = a.partial + (int64_t)blockIdx.z * a.M * a.N;
 #pragma unroll
         for (int i = 0; i < FM; ++i)
@@ -514,6 +517,84 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
                 }
             }
         return;
+    }
+    if (a.partial) {
+        // Split K, in-kernel sum: store the accumulators as they sit in registers (float4 q of
+        // fragment (i, j) of wave w at ((((w * FM + i) * FN + j) * 4 + q) * 64 + lane) * 16
+        // bytes into the block's slot of the tile), then count the tile's arrivals.  The
+        // last block to arrive sums the slots and goes on to the epilogue; the others
+        // are done.  No block waits for another.
+        //
+        // The slot stores and loads are device-coherent (sc1: they bypass the
+        // per-XCD L2 state that plain accesses may leave stale or unwritten), and each
+        // wave's stores are complete (vmcnt 0) before the barrier that precedes the
+        // count, so a block that sees the final count reads every slot's final data
+        // without a full L2 write-back / invalidate.
+        constexpr int SLOT = MT * NT;       // floats per slot
+        constexpr int CPOL_SC1 = 1 << 4;    // buffer cache policy: device-coherent
+        typedef float f32x4 __attribute__((ext_vector_type(4)));
+        const __amdgpu_buffer_rsrc_t rsP = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(a.partial + (int64_t)bid * a.splits * SLOT), (short)0, a.splits * SLOT * 4, 0x00020000);
+        const uint32_t vo_w = (uint32_t)((wave * FM * FN * 4 * 64 + lane) * 16);
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const f32x4 v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rsP,
+                                                           vo_w + ((i * FN + j) * 4 + q) * 1024,
+                                                           blockIdx.z * SLOT * 4, CPOL_SC1);
+                }
+        wait_vmcnt_lgkm0<0>();  // this wave's slot stores are complete
+        __syncthreads();        // ... for every wave; no wave still reads the ring
+        int* const flag = (int*)smem;
+        if (tid == 0) {
+            const unsigned prev = __hip_atomic_fetch_add(a.tile_cnt + bid, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const bool last = prev == (unsigned)a.splits - 1;
+            // ready for the next launch on this workspace
+            if (last) __hip_atomic_store(a.tile_cnt + bid, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            *flag = last;
+        }
+        __syncthreads();
+        if (!*flag) return;
+        // The tile is the sum of all slots in slot order (the own slot re-read), so
+        // the result does not depend on which block arrived last.  Slots go in rounds
+        // of SPR, every load of a round issued before any is added (slot indices
+        // clamped, repeats not added).
+        constexpr int SPR = FM * FN >= 4 ? 1 : 4 / (FM * FN);
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) acc[i][j] = floatx16{};
+        for (int z0 = 0; z0 < a.splits; z0 += SPR) {
+            f32x4 pv[SPR][FM][FN][4];
+#pragma unroll
+            for (int u = 0; u < SPR; ++u) {
+                const int so = min(z0 + u, a.splits - 1) * SLOT * 4;
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            pv[u][i][j][q] = __builtin_bit_cast(
+                                f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsP, vo_w + ((i * FN + j) * 4 + q) * 1024, so, CPOL_SC1));
+            }
+#pragma unroll
+            for (int u = 0; u < SPR; ++u) {
+                const bool use = z0 + u < a.splits;
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) acc[i][j][4 * q + e] += use ? pv[u][i][j][q][e] : 0.f;
+            }
+        }
     }
     // The fp32 tile goes through LDS (reusing the ring) in FM passes of WM*32 rows
     // (rows wm*TMW + i*32 + [0,32) of pass i).  In the vector path each thread owns
@@ -664,6 +745,17 @@ const char* const kNames[3][2] = {{"gemm_kernel<256,128,4,2,64,2,0>", "gemm_kern
 
 int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
+// In-kernel split-K sum: tile counters at the head of the workspace (one per tile),
+// the slots the summing block loads per round (as the kernel's SPR), and the
+// modelled cost of its tail.
+constexpr int kMaxSplitTiles = 16384;
+constexpr size_t kCounterBytes = kMaxSplitTiles * sizeof(unsigned);
+int fix_slots_per_round(int mt, int nt) {
+    const int f = (mt / 64) * (nt / 64);  // 32x32 fragments per wave (8 waves)
+    return f >= 4 ? 1 : 4 / f;
+}
+constexpr double kFixBase = 1.0e-6, kFixRound = 1.2e-6;
+
 // The epilogue keeps output statistics for two images per tile: the MT rows of a tile
 // (MT-aligned) must not reach a third image.
 bool stats_tile_ok(int mt, int hw) { return hw >= mt || mt == 2 * hw; }
@@ -672,11 +764,12 @@ bool stats_tile_ok(int mt, int hw) { return hw >= mt || mt == 2 * hw; }
 // spread evenly over the 256 CUs; the busiest CU runs its blocks two at a time where
 // the tile allows two per CU (a lone block cannot keep a CU busy: rate1 < rate2),
 // each round paying a fixed prologue / epilogue cost.  A split K adds the fp32
-// partial round trip (mostly L2 / Infinity Cache resident) and the reduce launch.
-void plan(const GemmArgs& a, int& ci, int& splits, int& kps) {
+// partial round trip (mostly L2 / Infinity Cache resident) and the serial tail of
+// the block that sums a tile's partials.
+void plan(const GemmArgs& a, int& ci, int& splits, int& kps, bool& fix) {
     const int nkt = ceil_div(a.K, 64);
     double best = 1e30;
-    ci = 1; splits = 1; kps = nkt * 64;
+    ci = 1; splits = 1; kps = nkt * 64; fix = false;
     for (int c = 0; c < 3; ++c) {
         const Cfg& g = kCfgs[c];
         if (a.geglu && g.nt < 128) continue;  // GEGLU pairs 32-column blocks within a 64-wide wave tile
@@ -695,9 +788,19 @@ void plan(const GemmArgs& a, int& ci, int& splits, int& kps) {
             // larger share of its time than a dense A: about 20% of its rate
             const double cf = (a.amode == A_CONV3 && g.nt < 128) ? 0.8 : 1.0;
             double t = pairs * (2.0 * w / (g.rate2 * cf) + g.t_fix) + singles * (w / (g.rate1 * cf) + g.t_fix);
-            // the reduce launch: about 5.5 us plus its traffic (2 us more with statistics)
-            if (se > 1) t += (double)se * a.M * a.N * 8.0 / 20.0e12 + (a.stats ? 7.5e-6 : 5.5e-6);
-            if (t < best * 0.98) { best = t; ci = c; splits = se; kps = kt_per * 64; }
+            // a split adds the partial round trip, and either the reduce launch (about
+            // 5.5 us, 2 us more with statistics) or the serial tail of each tile's last
+            // block (the count, then its rounds of slot loads)
+            bool fx = false;
+            if (se > 1) {
+                const double part = (double)se * a.M * a.N * 8.0 / 20.0e12;
+                const double t_red = part + (a.stats ? 7.5e-6 : 5.5e-6);
+                const int rounds = ceil_div(se, fix_slots_per_round(g.mt, g.nt));
+                const double t_fix = tiles <= kMaxSplitTiles ? part + kFixBase + kFixRound * rounds : 1e30;
+                fx = t_fix < t_red;
+                t += fx ? t_fix : t_red;
+            }
+            if (t < best * 0.98) { best = t; ci = c; splits = se; kps = kt_per * 64; fix = fx; }
         }
     }
 }
@@ -707,14 +810,21 @@ bool gemm_stats_supported(int hw) { return stats_tile_ok(128, hw); }
 
 const char* gemm_kernel_name(const GemmArgs& a) {
     int ci, splits, kps;
-    plan(a, ci, splits, kps);
+    bool fix;
+    plan(a, ci, splits, kps, fix);
     return kNames[ci][a.amode == A_CONV3];
 }
 
+size_t gemm_counter_bytes() { return kCounterBytes; }
+
 size_t gemm_workspace_bytes(const GemmArgs& a) {
     int ci, splits, kps;
-    plan(a, ci, splits, kps);
-    return splits > 1 ? (size_t)splits * a.M * a.N * sizeof(float) : 0;
+    bool fix;
+    plan(a, ci, splits, kps, fix);
+    if (splits == 1) return 0;
+    const Cfg& g = kCfgs[ci];
+    const size_t tiles = (size_t)ceil_div(a.M, g.mt) * ceil_div(a.N, g.nt);
+    return kCounterBytes + (fix ? tiles * g.mt * g.nt : (size_t)a.M * a.N) * splits * sizeof(float);
 }
 
 template <int AM>
@@ -726,11 +836,14 @@ static void launch_cfg(int ci, dim3 grid, const GemmArgs& a, hipStream_t s) {
 
 hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s) {
     int ci, splits, kps;
-    plan(a, ci, splits, kps);
+    bool fix;
+    plan(a, ci, splits, kps, fix);
     if (a.A2 == nullptr) a.K1 = a.K;
     a.splits = splits;
     a.k_per_split = kps;
-    a.partial = splits > 1 ? ws : nullptr;
+    a.fixup = fix;
+    a.tile_cnt = splits > 1 ? (unsigned*)ws : nullptr;
+    a.partial = splits > 1 ? (float*)((char*)ws + kCounterBytes) : nullptr;
     if (splits > 1 && ws == nullptr) return hipErrorInvalidValue;
     // operands are addressed with 32-bit byte offsets (buffer resources)
     const int64_t lim = 0x7fffffff;
@@ -751,13 +864,13 @@ hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s) {
                              (a.res ? 2.0 * a.M * nout : 0.0);
     const double part_bytes = splits > 1 ? 4.0 * splits * a.M * a.N : 0.0;
     const double flops = 2.0 * a.M * a.N * a.K;
-    const double k_bytes = a_bytes + 2.0 * a.N * a.K + (splits > 1 ? part_bytes : out_bytes);
+    const double k_bytes = a_bytes + 2.0 * a.N * a.K + (fix ? 2.0 * part_bytes + out_bytes : splits > 1 ? part_bytes : out_bytes);
     launch_timed(kNames[ci][a.amode == A_CONV3], flops, k_bytes, [&] {
         if (a.amode == A_DENSE) launch_cfg<A_DENSE>(ci, grid, a, s);
         else launch_cfg<A_CONV3>(ci, grid, a, s);
     });
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || splits == 1) return e;
+    if (e != hipSuccess || splits == 1 || fix) return e;
     const bool vec = a.out_mode != OUT_F32_NCHW && (a.N & 7) == 0;
     const int64_t total = (int64_t)a.M * (vec ? nout / 8 : nout);
     if (a.stats) {

@@ -62,8 +62,13 @@ struct GemmArgs {
     int out_mode;
     int hw_out;         // OUT_F32_NCHW: pixels per image
     int geglu;
-    // split-K
-    float* partial;     // [splits, M, N] fp32 (null: no split)
+    // split-K (set by gemm_launch).  fixup: each block of a tile stores its fp32
+    // partial tile into the tile's slots and the last of them to arrive (per-tile
+    // counter) sums the slots and runs the epilogue.  Otherwise the blocks store
+    // [splits, M, N] fp32 partials and a reduce kernel runs the epilogue.
+    float* partial;     // fixup: [tiles, splits, MT * NT] fp32 (null: no split)
+    unsigned* tile_cnt; // fixup: [tiles] arrival counters, zero on entry and left zero
+    int fixup;
     int splits;
     int k_per_split;    // multiple of the K tile
     // Optional per-channel statistics of the stored fp16 output, for a GroupNorm that
@@ -78,8 +83,11 @@ struct GemmArgs {
 // shape keeps each tile within two images).
 bool gemm_stats_supported(int hw);
 
-// Picks the tile shape and split-K factor; returns the fp32 workspace bytes the
-// launch needs (0 if none).  `ws` may be null when the return value is 0.
+// Picks the tile shape and split-K factor; returns the workspace bytes the launch
+// needs (0 if none).  `ws` may be null when the return value is 0.  A split launch
+// uses the first gemm_counter_bytes() of the workspace as tile counters: they must
+// be zero before the first launch on a workspace and every launch leaves them zero.
+size_t gemm_counter_bytes();
 size_t gemm_workspace_bytes(const GemmArgs& a);
 const char* gemm_kernel_name(const GemmArgs& a);  // tile variant the launch will use
 hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s);

@@ -562,6 +562,9 @@ static int plan_state(Ctx& c, FwdState& S) {
     hipError_t e;
     if ((e = mal((void**)&S.arena, S.arena_bytes)) != hipSuccess) return set_err(&c, SDU_ERR_OOM, "arena allocation failed");
     if ((e = mal((void**)&S.gemm_ws, dry.gemm_ws_need)) != hipSuccess) return set_err(&c, SDU_ERR_OOM, "gemm workspace");
+    // split-K tile counters start at zero (each launch leaves them zero)
+    if (dry.gemm_ws_need && (e = zero_launch(S.gemm_ws, gemm_counter_bytes(), c.stream)) != hipSuccess)
+        return hip_fail(c, e, "gemm workspace");
     const size_t lat_n = (size_t)(S.kind == 0 ? B : 1) * kLatC * HW;
     if ((e = mal((void**)&S.in_lat, lat_n * 4)) != hipSuccess) return set_err(&c, SDU_ERR_OOM, "staging");
     if ((e = mal((void**)&S.in_temb, (size_t)(S.kind == 0 ? 1 : S.steps) * 320 * 4)) != hipSuccess) return set_err(&c, SDU_ERR_OOM, "staging");

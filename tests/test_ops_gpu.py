@@ -95,6 +95,8 @@ def test_layernorm(op_engine, T, C):
     (512, 1280, 2560, 1280, True, False, False, False),  # 1x1 shortcut over a concat
     (77, 64, 64, 0, True, False, False, True),        # ragged M, N <= 64 tile, fp32 out
     (100, 128, 128, 0, True, False, True, False),     # GEGLU with ragged M
+    (64, 64, 8192, 0, True, True, False, False),      # one tile, many K splits
+    (200, 384, 3000, 0, True, False, False, True),    # split-K, ragged M and K tail, fp32 out
 ])
 def test_matmul(op_engine, M, N, K, K2, bias, res, geglu, f32):
     say(f"matmul M={M} N={N} K={K} K2={K2} bias={bias} res={res} geglu={geglu} f32={f32}")
@@ -130,6 +132,25 @@ def test_matmul(op_engine, M, N, K, K2, bias, res, geglu, f32):
     got = ty.numpy().astype(np.float32)
     assert rel_err_l1(got, ref) < 1e-3
     assert np.abs(got - ref).max() < 3e-2 * max(1.0, np.abs(ref).max() / 8)
+
+
+def test_matmul_split_repeat(op_engine):
+    """Split-K launches back to back: the per-tile arrival counters are left zero by
+    each launch, and the tile sums run in a fixed order, so repeats are bit-identical."""
+    say("matmul split-K repeat")
+    e = op_engine
+    outs = []
+    for M, N, K in [(128, 1280, 5120), (64, 64, 8192), (128, 1280, 5120)]:
+        a = r16((M, K), 21)
+        w = r16((N, K), 22, 0.05)
+        ta, tw = e.upload(a.astype(np.float16)), e.upload(w.astype(np.float16))
+        ty = e.tensor((M, N))
+        e.matmul(ta, tw, ty, M, N, K)
+        e.matmul(ta, tw, ty, M, N, K)
+        got = ty.numpy().astype(np.float32)
+        assert rel_err_l1(got, U.linear(t(a), t(w), None).numpy()) < 1e-3
+        outs.append(got)
+    assert np.array_equal(outs[0], outs[2])
 
 
 # ------------------------------------------------------------------ conv2d
