@@ -443,6 +443,38 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
         }
     };
 
+    // Epilogue thread mapping (vector path: one fixed 8-column slice per thread, rows
+    // r0 + k * rstep of each staged pass), and the residual rows of that slice.  Where
+    // they cost few registers (PRE) they are loaded here, so that their latency hides
+    // under the K loop; otherwise per pass in the epilogue.  Only a block that runs
+    // the epilogue loads them; no block writes output rows another block reads here.
+    constexpr int PR = WM * 32;                // staged rows per pass
+    constexpr int MAXR = PR * (NT / 8) / NTH;  // staged rows per thread per pass (non-GEGLU)
+    const bool narrow = a.out_mode == OUT_F32_NCHW || (a.N & 7);
+    const int NTO = NT / (a.geglu ? 2 : 1);  // output columns of this tile
+    const int cpr = NTO / 8;                  // 8-column chunks per row
+    const int oc = (tid % cpr) * 8;           // fixed output column slice of this thread
+    const int r0 = tid / cpr, rstep = NTH / cpr;
+    const int tc = a.geglu ? (oc >> 5) * 64 + (oc & 31) : oc;  // tile column of oc's source
+    const int n = n0 + tc;
+    const int nout = a.geglu ? (n0 >> 1) + oc : n;
+    constexpr bool PRE = FM * MAXR <= 2;
+    const bool use_res = a.res && !narrow && n < a.N && (!a.partial || a.fixup);
+    uint4 rres[FM][MAXR];
+    auto load_res = [&](int ip) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < MAXR; ++k) {
+            const int sr = r0 + k * rstep;
+            const int m = min(m0 + (sr >> 5) * TMW + ip * 32 + (sr & 31), a.M - 1);
+            rres[ip][k] = make_uint4(0, 0, 0, 0);
+            if (use_res && sr < PR) rres[ip][k] = *(const uint4*)(a.res + (int64_t)m * a.ldr + nout);
+        }
+    };
+    if (PRE) {
+#pragma unroll
+        for (int ip = 0; ip < FM; ++ip) load_res(ip);
+    }
+
     floatx16 acc[FM][FN];
 #pragma unroll
     for (int i = 0; i < FM; ++i)
@@ -598,21 +630,12 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
     }
     // The fp32 tile goes through LDS (reusing the ring) in FM passes of WM*32 rows
     // (rows wm*TMW + i*32 + [0,32) of pass i).  In the vector path each thread owns
-    // one fixed 8-column slice: bias / residual of a pass are all loaded before any
-    // store (the residual may alias the output), and stores are 16-byte.
-    constexpr int PR = WM * 32;  // staged rows per pass
+    // one fixed 8-column slice; the residual was loaded before any store (it may
+    // alias the output), and stores are 16-byte.
     constexpr int CST = NT + 4;  // padded fp32 row stride
     static_assert(PR * CST * 4 <= NS * STAGE * 2, "C pass fits the operand LDS");
     static_assert(NTH * 32 * 4 <= NS * STAGE * 2, "statistics flush fits the operand LDS");
     float* Cs = (float*)smem;
-    const bool narrow = a.out_mode == OUT_F32_NCHW || (a.N & 7);
-    const int NTO = NT / (a.geglu ? 2 : 1);  // output columns of this tile
-    const int cpr = NTO / 8;                  // 8-column chunks per row
-    const int oc = (tid % cpr) * 8;           // fixed output column slice of this thread
-    const int r0 = tid / cpr, rstep = NTH / cpr;
-    const int tc = a.geglu ? (oc >> 5) * 64 + (oc & 31) : oc;  // tile column of oc's source
-    const int n = n0 + tc;
-    const int nout = a.geglu ? (n0 >> 1) + oc : n;
     float badd[8], gadd[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) { badd[e] = 0.f; gadd[e] = 0.f; }
@@ -638,7 +661,6 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
             }
         }
     }
-    constexpr int MAXR = PR * (NT / 8) / NTH;  // staged rows per thread per pass (non-GEGLU)
     // per-channel output statistics (GroupNorm of the consumer): this thread's 8
     // columns over its rows, for the tile's first image (slot 0) and the next (slot 1)
     const bool do_st = a.stats != nullptr && !narrow;
@@ -673,16 +695,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
             continue;
         }
         if (n >= a.N) continue;
-        uint4 rres[MAXR];
-        if (a.res) {
-#pragma unroll
-            for (int k = 0; k < MAXR; ++k) {
-                const int sr = r0 + k * rstep;
-                const int m = m0 + (sr >> 5) * TMW + ip * 32 + (sr & 31);
-                rres[k] = make_uint4(0, 0, 0, 0);
-                if (sr < PR && m < a.M) rres[k] = *(const uint4*)(a.res + (int64_t)m * a.ldr + nout);
-            }
-        }
+        if (!PRE) load_res(ip);
 #pragma unroll
         for (int k = 0; k < MAXR; ++k) {
             const int sr = r0 + k * rstep;
@@ -695,7 +708,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
                 if (a.geglu) v[e] *= gelu_erf(Cs[sr * CST + tc + 32 + e] + gadd[e]);
             }
             if (a.res) {
-                const f16* rh = (const f16*)&rres[k];
+                const f16* rh = (const f16*)&rres[ip][k];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) v[e] += (float)rh[e];
             }
