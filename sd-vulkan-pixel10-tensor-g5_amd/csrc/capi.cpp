@@ -121,7 +121,17 @@ int sdu_set_weight(sdu_ctx* ctx, const char* name, const float* data, int64_t nu
         if (!r) return fail(ctx, SDU_ERR_WEIGHT, std::string("unknown weight: ") + name);
         if (numel != r->numel()) return fail(ctx, SDU_ERR_ARG, std::string("numel mismatch for ") + name);
         hipStreamSynchronize(ctx->c.stream);
-        return set_weight_canonical(ctx->c, *r, data);
+        int st = set_weight_canonical(ctx->c, *r, data);
+        if (st) return st;
+        // a source of a folded transformer-output weight: refold that transformer
+        const std::string n(name);
+        auto ends = [&](const char* suf) {
+            const size_t k = strlen(suf);
+            return n.size() >= k && n.compare(n.size() - k, k, suf) == 0;
+        };
+        if (ends(".ff.net.2.weight") || ends(".ff.net.2.bias") || ends(".proj_out.weight") || ends(".proj_out.bias"))
+            return fold_weights(ctx->c, n);
+        return SDU_OK;
     });
 }
 

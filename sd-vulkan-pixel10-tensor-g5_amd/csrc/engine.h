@@ -61,6 +61,9 @@ struct XfDesc {
     std::string pf;
     int c;
     int kv_off;  // column offset of this block's K in the fused cross K/V output
+    // feed-forward output and proj_out folded into one GEMM over [g | t] (fold_weights)
+    f16* w_out = nullptr;  // [C, 5C] = [Wp.Wf | Wp]
+    f16* b_out = nullptr;  // [C] = Wp.bf + bp
 };
 
 struct ProfAcc {
@@ -123,6 +126,9 @@ int build_inventory(Ctx& c);                       // fills weights / descs and 
 int init_weights_seeded(Ctx& c);
 int init_weights_dir(Ctx& c, const std::string& dir);
 int set_weight_canonical(Ctx& c, const WeightRec& r, const float* data);
+// Recompute the folded transformer-output weights from the loaded ones (all
+// transformers, or the one whose prefix `name` starts with); synchronous.
+int fold_weights(Ctx& c, const std::string& name = std::string());
 int get_weight_canonical(Ctx& c, const WeightRec& r, float* out);
 int ensure_op_ws(Ctx& c, size_t bytes);
 int set_err(Ctx* c, int code, const std::string& msg);

@@ -219,4 +219,83 @@ hipError_t gen_launch(f16* dst, const GenDesc& g, hipStream_t s) {
     return hipGetLastError();
 }
 
+
+// ----------------------------------------------------------------- weight folding
+//
+// A transformer's feed-forward output and its proj_out are consecutive linear maps
+// with a residual between them:
+//   t' = t + Wf.g + bf,   out = Wp.t' + bp + x
+// so out = [Wp.Wf | Wp] . [g | t] + (Wp.bf + bp) + x: one GEMM over the two-source
+// A = [g | t] with K = 5C instead of two GEMMs (same FLOPs, one launch and one
+// intermediate fewer).  wcat [C, 5C] row-major: columns [0, 4C) = Wp.Wf (fp32 sums
+// of fp16 products, rounded once), [4C, 5C) = Wp.  bcat [C] = Wp.bf + bp.
+
+namespace {
+constexpr int FT = 64;   // output tile (rows o x columns k)
+constexpr int FJ = 16;   // reduction chunk
+}
+
+// Block: 256 threads, a 64 x 64 tile of wcat, each thread 4 x 4 outputs.
+__global__ __launch_bounds__(256) void fold_ffout_kernel(const f16* Wp, const f16* Wf, f16* wcat, int C) {
+    __shared__ float sp[FT][FJ + 1];  // Wp[o0 + r][j0 + c]
+    __shared__ float sf[FJ][FT + 1];  // Wf[j0 + r][k0 + c]
+    const int K4 = 4 * C, K5 = 5 * C;
+    const int k0 = blockIdx.x * FT, o0 = blockIdx.y * FT;
+    const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+    if (k0 >= K4) {  // the Wp copy columns
+        for (int i = threadIdx.x; i < FT * FT; i += 256) {
+            const int o = o0 + i / FT, k = k0 + i % FT;
+            if (o < C && k < K5) wcat[(int64_t)o * K5 + k] = Wp[(int64_t)o * C + (k - K4)];
+        }
+        return;
+    }
+    float acc[4][4] = {};
+    for (int j0 = 0; j0 < C; j0 += FJ) {
+        for (int i = threadIdx.x; i < FT * FJ; i += 256) {
+            const int r = i / FJ, c = i % FJ;
+            const int o = o0 + r, j = j0 + c;
+            sp[r][c] = (o < C && j < C) ? (float)Wp[(int64_t)o * C + j] : 0.f;
+            const int r2 = i / FT, c2 = i % FT;
+            const int j2 = j0 + r2, k = k0 + c2;
+            sf[r2][c2] = (j2 < C && k < K4) ? (float)Wf[(int64_t)j2 * K4 + k] : 0.f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < FJ; ++j) {
+            float a[4], b[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) { a[u] = sp[ty * 4 + u][j]; b[u] = sf[j][tx * 4 + u]; }
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[u][v] = fmaf(a[u], b[v], acc[u][v]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int o = o0 + ty * 4 + u, k = k0 + tx * 4 + v;
+            if (o < C && k < K4) wcat[(int64_t)o * K5 + k] = (f16)acc[u][v];
+        }
+}
+
+__global__ void fold_ffout_bias_kernel(const f16* Wp, const f16* bf, const f16* bp, f16* bcat, int C) {
+    const int o = blockIdx.x * blockDim.x + threadIdx.x;
+    if (o >= C) return;
+    float s = 0.f;
+    for (int j = 0; j < C; ++j) s = fmaf((float)Wp[(int64_t)o * C + j], (float)bf[j], s);
+    bcat[o] = (f16)(s + (float)bp[o]);
+}
+
+hipError_t fold_ffout_launch(const f16* Wp, const f16* bp, const f16* Wf, const f16* bf, f16* wcat, f16* bcat,
+                             int C, hipStream_t s) {
+    if (C <= 0 || C % 16) return hipErrorInvalidValue;  // 4C: whole 64-column tiles
+    hipLaunchKernelGGL(fold_ffout_kernel, dim3((5 * C + FT - 1) / FT, (C + FT - 1) / FT), dim3(256), 0, s, Wp, Wf,
+                       wcat, C);
+    hipLaunchKernelGGL(fold_ffout_bias_kernel, dim3((C + 255) / 256), dim3(256), 0, s, Wp, bf, bp, bcat, C);
+    return hipGetLastError();
+}
+
 }  // namespace sdu

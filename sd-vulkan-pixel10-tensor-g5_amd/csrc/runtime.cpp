@@ -187,6 +187,12 @@ int build_inventory(Ctx& c) {
         if (d == -2) { off[i] = top; top += align(c.weights[i].dev_n); }
         else if (d == -3) { off[i] = top; top += align(3 * c.weights[i].dev_n); }
     }
+    std::vector<int64_t> off_fold(c.xfs.size());
+    for (size_t i = 0; i < c.xfs.size(); ++i) {
+        const int64_t ch = c.xfs[i].c;
+        off_fold[i] = top;
+        top += align(5 * ch * ch) + align(ch);
+    }
     c.wpool_bytes = (size_t)top * sizeof(f16);
     hipError_t e = hipMalloc(&c.wpool, c.wpool_bytes);
     if (e != hipSuccess) return set_err(&c, SDU_ERR_OOM, "weight pool allocation failed");
@@ -204,11 +210,28 @@ int build_inventory(Ctx& c) {
         c.weights[c.widx[rd.pf + ".time_emb_proj.weight"]].dev = c.w_tproj + (int64_t)rd.tproj_off * kTembDim;
         c.weights[c.widx[rd.pf + ".time_emb_proj.bias"]].dev = c.b_tproj + rd.tproj_off;
     }
-    for (const XfDesc& xd : c.xfs) {
+    for (size_t i = 0; i < c.xfs.size(); ++i) {
+        XfDesc& xd = c.xfs[i];
         const std::string b = xd.pf + ".transformer_blocks.0";
         c.weights[c.widx[b + ".attn2.to_k.weight"]].dev = c.w_kv + (int64_t)xd.kv_off * kCtxDim;
         c.weights[c.widx[b + ".attn2.to_v.weight"]].dev = c.w_kv + (int64_t)(xd.kv_off + xd.c) * kCtxDim;
+        xd.w_out = P + off_fold[i];
+        xd.b_out = xd.w_out + align(5 * (int64_t)xd.c * xd.c);
     }
+    return SDU_OK;
+}
+
+int fold_weights(Ctx& c, const std::string& name) {
+    for (const XfDesc& xd : c.xfs) {
+        if (!name.empty() && name.compare(0, xd.pf.size() + 1, xd.pf + ".") != 0) continue;
+        const std::string b = xd.pf + ".transformer_blocks.0";
+        hipError_t e = fold_ffout_launch(c.wd(xd.pf + ".proj_out.weight"), c.wd(xd.pf + ".proj_out.bias"),
+                                         c.wd(b + ".ff.net.2.weight"), c.wd(b + ".ff.net.2.bias"), xd.w_out,
+                                         xd.b_out, xd.c, c.stream);
+        if (e != hipSuccess) return set_err(&c, SDU_ERR_HIP, std::string("weight fold: ") + hipGetErrorString(e));
+    }
+    hipError_t e = hipStreamSynchronize(c.stream);
+    if (e != hipSuccess) return set_err(&c, SDU_ERR_HIP, hipGetErrorString(e));
     return SDU_OK;
 }
 
@@ -256,9 +279,7 @@ int init_weights_seeded(Ctx& c) {
         hipError_t e = gen_launch(r.dev, g, c.stream);
         if (e != hipSuccess) return set_err(&c, SDU_ERR_HIP, std::string("weight generator: ") + hipGetErrorString(e));
     }
-    hipError_t e = hipStreamSynchronize(c.stream);
-    if (e != hipSuccess) return set_err(&c, SDU_ERR_HIP, hipGetErrorString(e));
-    return SDU_OK;
+    return fold_weights(c);
 }
 
 // canonical fp16 bits -> device layout, upload
@@ -300,7 +321,7 @@ int init_weights_dir(Ctx& c, const std::string& dir) {
         int st = upload_canonical_f16(c, r, src);
         if (st) return st;
     }
-    return SDU_OK;
+    return fold_weights(c);
 }
 
 int set_weight_canonical(Ctx& c, const WeightRec& r, const float* data) {

@@ -161,6 +161,11 @@ struct GenDesc {
     int constant;      // 1: fill `mean` (no randomness)
 };
 hipError_t gen_launch(f16* dst, const GenDesc& g, hipStream_t s);
+
+// Transformer output fold (init time): wcat [C, 5C] = [Wp.Wf | Wp], bcat [C] = Wp.bf + bp,
+// for proj_out (Wp [C, C], bp) after the feed-forward output (Wf [C, 4C], bf).  C % 16 == 0.
+hipError_t fold_ffout_launch(const f16* Wp, const f16* bp, const f16* Wf, const f16* bf, f16* wcat, f16* bcat,
+                             int C, hipStream_t s);
 // n fp32 N(0,1) values of the same generator (element i from key, no fp16 rounding).
 hipError_t gen_normal_f32_launch(float* dst, int64_t n, uint64_t key, hipStream_t s);
 

@@ -256,7 +256,10 @@ static Act transformer(Exec& E, const XfDesc& t, Act xa, int H, int Wd, const f1
         a.res = tt; a.ldr = C;
         gemm(E, "linear", a);
     }
-    // GEGLU feed-forward: proj (+bias, GEGLU in the epilogue) then out (+bias, +residual)
+    // GEGLU feed-forward: proj (+bias, GEGLU in the epilogue).  Its output projection
+    // (+bias, +residual t) and proj_out (+bias, +residual x) are one GEMM over the
+    // two-source A = [ff | t] with the folded weight [Wp.Wf | Wp] (fold_weights):
+    // out = Wp.(t + Wf.ff + bf) + bp + x.
     layernorm(E, tt, W(E, b + ".norm3.weight"), W(E, b + ".norm3.bias"), h, M, C);
     f16* ff = E.alloc<f16>((size_t)M * 4 * C);
     {
@@ -265,20 +268,15 @@ static Act transformer(Exec& E, const XfDesc& t, Act xa, int H, int Wd, const f1
         a.geglu = 1;
         gemm(E, "linear_geglu", a);
     }
-    {
-        GemmArgs a = dense_args(ff, 4 * C, M, C, 4 * C, W(E, b + ".ff.net.2.weight"), tt, C);
-        a.bias = W(E, b + ".ff.net.2.bias");
-        a.res = tt; a.ldr = C;
-        gemm(E, "linear", a);
-    }
     Act o{out, nullptr};
     {
-        GemmArgs a = dense_args(tt, C, M, C, C, W(E, t.pf + ".proj_out.weight"), out, C);
-        a.bias = W(E, t.pf + ".proj_out.bias");
+        GemmArgs a = dense_args(ff, 4 * C, M, C, 5 * C, t.w_out, out, C);
+        a.A2 = tt; a.lda2 = C; a.K1 = 4 * C;
+        a.bias = t.b_out;
         a.res = x; a.ldr = C;
         want_stats(E, a, HW);
         o.st = a.stats;
-        gemm(E, "conv1x1", a);
+        gemm(E, "linear_out", a);
     }
     E.ar->release(mk);
     return o;

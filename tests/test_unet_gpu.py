@@ -133,6 +133,37 @@ def test_forward_b2_96(unet_engine, oracle_weights):
     assert e <= TOL
 
 
+def test_set_weight_refolds(unet_engine, oracle_weights):
+    """The feed-forward output and proj_out of a transformer run as one GEMM over a
+    folded weight.  Setting any of their four source tensors through sdu_set_weight
+    refolds it: the forward matches the oracle run with the same new weights."""
+    pf = "up_blocks.3.attentions.1"
+    names = [pf + ".transformer_blocks.0.ff.net.2.weight", pf + ".transformer_blocks.0.ff.net.2.bias",
+             pf + ".proj_out.weight", pf + ".proj_out.bias"]
+    specs = {p.name: p for p in Wt.param_specs()}
+    rng = np.random.default_rng(5)
+    p2 = dict(oracle_weights)
+    orig = {}
+    try:
+        for n in names:
+            shape = specs[n].shape
+            v = (rng.standard_normal(shape) * 0.05).astype(np.float16).astype(np.float32)
+            orig[n] = unet_engine.get_weight(n, shape)
+            unet_engine.set_weight(n, v)
+            p2[n] = torch.from_numpy(v)
+        lat, temb, ctx = inputs(1, 32, 32, seed=17)
+        say("forward B=1 32x32 after set_weight on folded sources")
+        got = unet_engine.forward(lat, temb, ctx)
+        e = rel_err_l1(got, oracle_forward(p2, lat, temb, ctx))
+        e_old = rel_err_l1(got, oracle_forward(oracle_weights, lat, temb, ctx))
+        say(f"relErr new weights = {e:.3e}, vs old weights = {e_old:.3e}")
+        assert e <= TOL
+        assert e_old > max(TOL, 5 * e)  # the change is visible in the output
+    finally:
+        for n, v in orig.items():
+            unet_engine.set_weight(n, v)
+
+
 def test_forward_b16_matches_pairs(unet_engine):
     """B=16 throughput batch: eight copies of one CFG pair must each reproduce the
     B=2 result (per-image independence of every kernel; split-K factors differ
