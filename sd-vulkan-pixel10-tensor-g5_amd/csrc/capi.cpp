@@ -123,13 +123,14 @@ int sdu_set_weight(sdu_ctx* ctx, const char* name, const float* data, int64_t nu
         hipStreamSynchronize(ctx->c.stream);
         int st = set_weight_canonical(ctx->c, *r, data);
         if (st) return st;
-        // a source of a folded transformer-output weight: refold that transformer
+        // a source of a folded weight: refold that block
         const std::string n(name);
         auto ends = [&](const char* suf) {
             const size_t k = strlen(suf);
             return n.size() >= k && n.compare(n.size() - k, k, suf) == 0;
         };
-        if (ends(".ff.net.2.weight") || ends(".ff.net.2.bias") || ends(".proj_out.weight") || ends(".proj_out.bias"))
+        if (ends(".ff.net.2.weight") || ends(".ff.net.2.bias") || ends(".proj_out.weight") || ends(".proj_out.bias") ||
+            ends(".conv2.weight") || ends(".conv2.bias") || ends(".conv_shortcut.weight") || ends(".conv_shortcut.bias"))
             return fold_weights(ctx->c, n);
         return SDU_OK;
     });

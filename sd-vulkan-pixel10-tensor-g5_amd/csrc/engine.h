@@ -56,6 +56,9 @@ struct ResDesc {
     std::string pf;
     int cin, cout, cin1;  // cin1: channels from the first source (concat split)
     int tproj_off;
+    // cin != cout: conv2 and the 1x1 shortcut folded into one GEMM (fold_weights)
+    f16* w2sc = nullptr;  // [cout, 9 cout + cin] = [conv2 | shortcut]
+    f16* b2sc = nullptr;  // [cout] = b2 + bs
 };
 struct XfDesc {
     std::string pf;
@@ -126,8 +129,8 @@ int build_inventory(Ctx& c);                       // fills weights / descs and 
 int init_weights_seeded(Ctx& c);
 int init_weights_dir(Ctx& c, const std::string& dir);
 int set_weight_canonical(Ctx& c, const WeightRec& r, const float* data);
-// Recompute the folded transformer-output weights from the loaded ones (all
-// transformers, or the one whose prefix `name` starts with); synchronous.
+// Recompute the folded weights (transformer output, resnet conv2 + shortcut) from
+// the loaded ones (all blocks, or the one whose prefix `name` starts with); synchronous.
 int fold_weights(Ctx& c, const std::string& name = std::string());
 int get_weight_canonical(Ctx& c, const WeightRec& r, float* out);
 int ensure_op_ws(Ctx& c, size_t bytes);

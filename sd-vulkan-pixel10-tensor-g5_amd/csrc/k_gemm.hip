@@ -7,7 +7,9 @@
 //     source (the 1x1 shortcut over the up-path concat, vk_engine.cpp:634, :754).
 //   * A_CONV3: A is the implicit im2col of an NHWC image for a 3x3 conv, pad 1,
 //     stride 1/2 (downsample, :689-692), optional nearest-2x upsample folded into
-//     the index math (upsample, :693-697).  K index = tap*Cin + ci.
+//     the index math (upsample, :693-697).  K index = tap*Cin + ci.  Columns past
+//     9*Cin may come from one or two dense sources of the same pixels: a resnet's
+//     1x1 shortcut (:634) summed into its conv2.
 // Epilogue (fused; the reference runs these as separate AB/AB2/ADD/GEGLU passes):
 // + bias[n] + bias2[n] (fp32 time projection), GEGLU over interleaved a/b column
 // blocks, + residual, store fp16 / fp32 / fp32-NCHW.
@@ -338,7 +340,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
     int a_c[AI];          // element offset of the lane's chunk within the K tile
     int a_m[AI];          // dense: row (clamped)
     uint32_t voA[AI];     // dense: byte offset of (row, chunk) in A
-    uint32_t voA2[AI];    // dense: byte offset of (row, chunk) in A2
+    uint32_t voA2[AI];    // byte offset of (row, chunk) in A2 (dense second source, conv tail)
+    uint32_t voA3[AI];    // conv: byte offset of (row, chunk) in A3
     int a_off[AI];        // conv: element offset of tap (0,0) of the lane's output pixel (+chunk)
     int a_vm[AI];         // conv: bit ky*3+kx set when that tap is inside the image
     int a_b[AI], a_oy[AI], a_ox[AI];  // conv geometry for the per-lane path
@@ -352,6 +355,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
             voA[i] = (uint32_t)((m * a.lda + a_c[i]) * 2);
             voA2[i] = a.A2 ? (uint32_t)((m * a.lda2 + a_c[i]) * 2) : 0u;
         } else {
+            voA2[i] = a.A2 ? (uint32_t)((m * a.lda2 + a_c[i]) * 2) : 0u;
+            voA3[i] = a.A3 ? (uint32_t)((m * a.lda3 + a_c[i]) * 2) : 0u;
             const int hw = a.Ho * a.Wo;
             const int bb = m / hw, p = m - bb * hw;
             const int oy = p / a.Wo, ox = p - oy * a.Wo;
@@ -375,6 +380,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
         AM == A_DENSE ? a.M * a.lda * 2 : a.Bn * a.Hin * a.Win * a.Cin * 2, 0x00020000);
     const __amdgpu_buffer_rsrc_t rsA2 = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(a.A2 ? a.A2 : a.A), (short)0, a.A2 ? a.M * a.lda2 * 2 : 0, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsA3 = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(a.A3 ? a.A3 : a.A), (short)0, a.A3 ? a.M * a.lda3 * 2 : 0, 0x00020000);
     // conv fast path: each K tile lies inside one tap (Cin % BKT == 0) and the input
     // is not upsampled, so the tap offset is one scalar per tile
     const bool conv_fast = AM == A_CONV3 && a.Cin % BKT == 0 && !a.upsample;
@@ -409,6 +416,16 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
                                                          : a.A + (int64_t)a_m[i] * a.lda + k;
                     dma(k < kend ? src : zero, sA + (i * NW + wave) * RPI * BKT);
                 }
+            }
+        } else if (a.A2 && k0 >= a.K1) {
+            // conv dense tail: whole tiles (K1, K2, K multiples of the K tile), after
+            // every conv tile, so the fast path's tap counters are not advanced
+            if (!a.A3 || k0 < a.K2) {
+#pragma unroll
+                for (int i = 0; i < AI; ++i) bdma(rsA2, voA2[i], (k0 - a.K1) * 2, sA + (i * NW + wave) * RPI * BKT);
+            } else {
+#pragma unroll
+                for (int i = 0; i < AI; ++i) bdma(rsA3, voA3[i], (k0 - a.K2) * 2, sA + (i * NW + wave) * RPI * BKT);
             }
         } else if (conv_fast) {
             const int tap = tap_next, ky = tap / 3, kx = tap - ky * 3;
@@ -852,6 +869,13 @@ hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s) {
     bool fix;
     plan(a, ci, splits, kps, fix);
     if (a.A2 == nullptr) a.K1 = a.K;
+    if (a.A3 == nullptr) a.K2 = a.K;
+    if (a.A3 && (a.amode != A_CONV3 || !a.A2)) return hipErrorInvalidValue;
+    if (a.amode == A_CONV3 && a.A2 &&
+        (a.K1 != 9 * a.Cin || a.K1 % 64 || a.K2 % 64 || a.K % 64 || a.K2 <= a.K1 || a.K <= a.K1 ||
+         (a.A3 && a.K2 >= a.K) || a.stride != 1 || a.upsample || a.Ho != a.Hin || a.Wo != a.Win ||
+         a.M != a.Bn * a.Ho * a.Wo || a.lda2 < a.K2 - a.K1 || (a.A3 && a.lda3 < a.K - a.K2)))
+        return hipErrorInvalidValue;
     a.splits = splits;
     a.k_per_split = kps;
     a.fixup = fix;
@@ -863,7 +887,9 @@ hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s) {
     if (2 * (int64_t)a.N * a.K > lim) return hipErrorInvalidValue;
     if (a.amode == A_DENSE && (2 * (int64_t)a.M * a.lda > lim || (a.A2 && 2 * (int64_t)a.M * a.lda2 > lim)))
         return hipErrorInvalidValue;
-    if (a.amode == A_CONV3 && 2 * (int64_t)a.Bn * a.Hin * a.Win * a.Cin > lim) return hipErrorInvalidValue;
+    if (a.amode == A_CONV3 && (2 * (int64_t)a.Bn * a.Hin * a.Win * a.Cin > lim ||
+                               (a.A2 && 2 * (int64_t)a.M * a.lda2 > lim) || (a.A3 && 2 * (int64_t)a.M * a.lda3 > lim)))
+        return hipErrorInvalidValue;
     const Cfg& g = kCfgs[ci];
     if (a.stats && (a.out_mode != OUT_F16 || a.geglu || (a.N & 7) || a.stats_hw < 64 ||
                     !stats_tile_ok(g.mt, a.stats_hw)))
@@ -872,7 +898,8 @@ hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s) {
     // algorithmic traffic: A once (the conv source image, not its im2col), W once, output
     // (+ residual) once; a split pays its fp32 partials out and back
     const int nout = a.geglu ? a.N / 2 : a.N;
-    const double a_bytes = a.amode == A_CONV3 ? 2.0 * a.Bn * a.Hin * a.Win * a.Cin : 2.0 * a.M * a.K;
+    const double a_bytes = a.amode == A_CONV3 ? 2.0 * a.Bn * a.Hin * a.Win * a.Cin + 2.0 * a.M * (a.K - a.K1)
+                                              : 2.0 * a.M * a.K;
     const double out_bytes = (double)a.M * nout * (a.out_mode == OUT_F16 ? 2.0 : 4.0) +
                              (a.res ? 2.0 * a.M * nout : 0.0);
     const double part_bytes = splits > 1 ? 4.0 * splits * a.M * a.N : 0.0;

@@ -298,4 +298,22 @@ hipError_t fold_ffout_launch(const f16* Wp, const f16* bp, const f16* Wf, const 
     return hipGetLastError();
 }
 
+// A resnet's 1x1 shortcut summed into its conv2: wcat [Co, 9 Ci2 + Cs] rows =
+// [conv2 row (OHWI, 9 Ci2) | shortcut row (Cs)], bcat = b2 + bs.
+__global__ void fold_shortcut_kernel(const f16* w2, const f16* b2, const f16* ws, const f16* bs, f16* wcat,
+                                     f16* bcat, int Co, int K2, int Cs) {
+    const int o = blockIdx.y;
+    const int K = K2 + Cs;
+    for (int k = blockIdx.x * blockDim.x + threadIdx.x; k < K; k += gridDim.x * blockDim.x)
+        wcat[(int64_t)o * K + k] = k < K2 ? w2[(int64_t)o * K2 + k] : ws[(int64_t)o * Cs + (k - K2)];
+    if (blockIdx.x == 0 && threadIdx.x == 0) bcat[o] = (f16)((float)b2[o] + (float)bs[o]);
+}
+
+hipError_t fold_shortcut_launch(const f16* w2, const f16* b2, const f16* ws, const f16* bs, f16* wcat, f16* bcat,
+                                int Co, int Ci2, int Cs, hipStream_t s) {
+    if (Co <= 0 || Ci2 <= 0 || Cs <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(fold_shortcut_kernel, dim3(8, Co), dim3(256), 0, s, w2, b2, ws, bs, wcat, bcat, Co, 9 * Ci2, Cs);
+    return hipGetLastError();
+}
+
 }  // namespace sdu

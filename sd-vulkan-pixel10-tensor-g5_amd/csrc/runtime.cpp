@@ -187,11 +187,17 @@ int build_inventory(Ctx& c) {
         if (d == -2) { off[i] = top; top += align(c.weights[i].dev_n); }
         else if (d == -3) { off[i] = top; top += align(3 * c.weights[i].dev_n); }
     }
-    std::vector<int64_t> off_fold(c.xfs.size());
+    std::vector<int64_t> off_fold(c.xfs.size()), off_rfold(c.resnets.size(), -1);
     for (size_t i = 0; i < c.xfs.size(); ++i) {
         const int64_t ch = c.xfs[i].c;
         off_fold[i] = top;
         top += align(5 * ch * ch) + align(ch);
+    }
+    for (size_t i = 0; i < c.resnets.size(); ++i) {
+        const ResDesc& rd = c.resnets[i];
+        if (rd.cin == rd.cout) continue;
+        off_rfold[i] = top;
+        top += align((int64_t)rd.cout * (9 * rd.cout + rd.cin)) + align(rd.cout);
     }
     c.wpool_bytes = (size_t)top * sizeof(f16);
     hipError_t e = hipMalloc(&c.wpool, c.wpool_bytes);
@@ -206,9 +212,14 @@ int build_inventory(Ctx& c) {
         if (d == -2 || d == -3) r.dev = P + off[i];
         else if (d == -4) r.dev = c.weights[i - 1].dev + c.weights[i - 1].dev_n;  // k after q, v after k
     }
-    for (const ResDesc& rd : c.resnets) {
+    for (size_t i = 0; i < c.resnets.size(); ++i) {
+        ResDesc& rd = c.resnets[i];
         c.weights[c.widx[rd.pf + ".time_emb_proj.weight"]].dev = c.w_tproj + (int64_t)rd.tproj_off * kTembDim;
         c.weights[c.widx[rd.pf + ".time_emb_proj.bias"]].dev = c.b_tproj + rd.tproj_off;
+        if (off_rfold[i] >= 0) {
+            rd.w2sc = P + off_rfold[i];
+            rd.b2sc = rd.w2sc + align((int64_t)rd.cout * (9 * rd.cout + rd.cin));
+        }
     }
     for (size_t i = 0; i < c.xfs.size(); ++i) {
         XfDesc& xd = c.xfs[i];
@@ -222,6 +233,14 @@ int build_inventory(Ctx& c) {
 }
 
 int fold_weights(Ctx& c, const std::string& name) {
+    for (const ResDesc& rd : c.resnets) {
+        if (rd.cin == rd.cout) continue;
+        if (!name.empty() && name.compare(0, rd.pf.size() + 1, rd.pf + ".") != 0) continue;
+        hipError_t e = fold_shortcut_launch(c.wd(rd.pf + ".conv2.weight"), c.wd(rd.pf + ".conv2.bias"),
+                                            c.wd(rd.pf + ".conv_shortcut.weight"), c.wd(rd.pf + ".conv_shortcut.bias"),
+                                            rd.w2sc, rd.b2sc, rd.cout, rd.cout, rd.cin, c.stream);
+        if (e != hipSuccess) return set_err(&c, SDU_ERR_HIP, std::string("weight fold: ") + hipGetErrorString(e));
+    }
     for (const XfDesc& xd : c.xfs) {
         if (!name.empty() && name.compare(0, xd.pf.size() + 1, xd.pf + ".") != 0) continue;
         const std::string b = xd.pf + ".transformer_blocks.0";

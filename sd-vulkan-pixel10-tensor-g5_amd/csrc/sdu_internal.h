@@ -36,7 +36,9 @@ inline void launch_timed(const char* kernel, double flops, double bytes, const F
 // C[M,N] = A[M,K] . W[N,K]^T with a fused epilogue.  A is either a dense
 // row-major matrix (optionally split over two sources along K) or the implicit
 // im2col of an NHWC image for a 3x3 conv (pad 1, stride 1/2, optional 2x
-// nearest upsample of the input).
+// nearest upsample of the input), optionally followed along K by up to two dense
+// sources (a 1x1 conv over another tensor of the same pixels, summed into the
+// same outputs).
 enum AMode { A_DENSE = 0, A_CONV3 = 1 };
 enum OutMode { OUT_F16 = 0, OUT_F32 = 1, OUT_F32_NCHW = 2 };
 
@@ -46,9 +48,12 @@ struct GemmArgs {
     int amode;
     const f16* A;     // dense: [M, lda]; conv: NHWC input [B, Hin, Win, Cin]
     int lda;
-    const f16* A2;    // dense only: columns [K1, K) come from A2 [M, lda2]
-    int lda2;
-    int K1;           // dense: split point (K when A2 == nullptr)
+    const f16* A2;    // dense: columns [K1, K) come from A2 [M, lda2]; conv: columns
+    int lda2;         //   [K1 = 9 Cin, K2) from A2 and [K2, K) from A3 [M, lda3]
+    int K1;           // split point (K when A2 == nullptr)
+    const f16* A3;    // conv only (stride 1, no upsample; K1, K2, K multiples of 64)
+    int lda3;
+    int K2;           // (K when A3 == nullptr)
     int Bn, Hin, Win, Cin, Ho, Wo, stride, upsample;  // conv geometry
     // B operand: W [N, K] row-major
     const f16* Wt;
@@ -166,6 +171,10 @@ hipError_t gen_launch(f16* dst, const GenDesc& g, hipStream_t s);
 // for proj_out (Wp [C, C], bp) after the feed-forward output (Wf [C, 4C], bf).  C % 16 == 0.
 hipError_t fold_ffout_launch(const f16* Wp, const f16* bp, const f16* Wf, const f16* bf, f16* wcat, f16* bcat,
                              int C, hipStream_t s);
+// Resnet shortcut fold (init time): wcat [Co, 9 Ci2 + Cs] = [conv2 (OHWI) | shortcut],
+// bcat = b2 + bs, for conv2 over Ci2 channels and a 1x1 shortcut over Cs channels.
+hipError_t fold_shortcut_launch(const f16* w2, const f16* b2, const f16* ws, const f16* bs, f16* wcat, f16* bcat,
+                                int Co, int Ci2, int Cs, hipStream_t s);
 // n fp32 N(0,1) values of the same generator (element i from key, no fp16 rounding).
 hipError_t gen_normal_f32_launch(float* dst, int64_t n, uint64_t key, hipStream_t s);
 

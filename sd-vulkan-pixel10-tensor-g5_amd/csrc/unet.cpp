@@ -194,20 +194,23 @@ static Act resnet(Exec& E, const ResDesc& r, Act x, Act x2, int H, int Wd, const
     f16* h2 = E.alloc<f16>((size_t)M * r.cout);
     groupnorm(E, hca, Act{nullptr, nullptr}, r.cout, 0, W(E, r.pf + ".norm2.weight"),
               W(E, r.pf + ".norm2.bias"), h2, HW, 1);
-    const f16* res = x.p;
-    if (r.cin != r.cout) {  // 1x1 shortcut over (possibly concatenated) input (:634)
-        f16* sx = E.alloc<f16>((size_t)M * r.cout);
-        GemmArgs a = dense_args(x.p, r.cin1, M, r.cout, r.cin, W(E, r.pf + ".conv_shortcut.weight"), sx, r.cout);
-        if (x2.p) { a.A2 = x2.p; a.lda2 = r.cin - r.cin1; a.K1 = r.cin1; }
-        a.bias = W(E, r.pf + ".conv_shortcut.bias");
-        gemm(E, "conv1x1", a);
-        res = sx;
-    }
     Act o{out, nullptr};
     {
         GemmArgs a = conv3_args(h2, B, H, Wd, r.cout, r.cout, 1, 0, W(E, r.pf + ".conv2.weight"), out);
         a.bias = W(E, r.pf + ".conv2.bias");
-        a.res = res; a.ldr = r.cout;
+        if (r.cin != r.cout) {
+            // the 1x1 shortcut over the (possibly concatenated) input (:634) is extra K
+            // columns of conv2: A = [im2col(h2) | x | x2], W = [conv2 | shortcut]
+            a.Wt = r.w2sc;
+            a.bias = r.b2sc;
+            a.K1 = 9 * r.cout;
+            a.A2 = x.p; a.lda2 = r.cin1;
+            a.K2 = a.K1 + r.cin1;
+            if (x2.p) { a.A3 = x2.p; a.lda3 = r.cin - r.cin1; }
+            a.K = a.K1 + r.cin;
+        } else {
+            a.res = x.p; a.ldr = r.cout;
+        }
         want_stats(E, a, HW);
         o.st = a.stats;
         gemm(E, "conv3x3", a);
