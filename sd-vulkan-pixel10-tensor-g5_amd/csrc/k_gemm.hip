@@ -838,6 +838,13 @@ void plan(const GemmArgs& a, int& ci, int& splits, int& kps, bool& fix) {
 
 bool gemm_stats_supported(int hw) { return stats_tile_ok(128, hw); }
 
+bool gemm_uses_reduce_kernel(const GemmArgs& a) {
+    int ci, splits, kps;
+    bool fix;
+    plan(a, ci, splits, kps, fix);
+    return splits > 1 && !fix;
+}
+
 const char* gemm_kernel_name(const GemmArgs& a) {
     int ci, splits, kps;
     bool fix;

@@ -95,6 +95,7 @@ bool gemm_stats_supported(int hw);
 size_t gemm_counter_bytes();
 size_t gemm_workspace_bytes(const GemmArgs& a);
 const char* gemm_kernel_name(const GemmArgs& a);  // tile variant the launch will use
+bool gemm_uses_reduce_kernel(const GemmArgs& a);  // split K summed by a separate reduce launch
 hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s);
 
 // y[n] = act_out( sum_k act_in(x[k]) * W[n,k] + bias[n] ), fp32 in/out, W fp16 [N,K].
