@@ -107,7 +107,7 @@ __device__ __forceinline__ void reduce_scalar(const GemmArgs& a, int m, int nout
 
 // Sum the split-K partials of 8 output columns (nout ..) for R rows m[r] and apply the
 // epilogue; rows whose bit in `valid` is clear are read (m clamped by the caller) but
-// not stored.  Every load of a round of 4 splits over all R rows is issued before any
+// not stored.  Every load of a round of U splits over all R rows is issued before any
 // is added (the last round re-reads split splits-1 and weights the repeats 0), and
 // the bias / residual loads come first.  GG = false: no GEGLU.  ov[r] = the stored
 // fp16 values (OUT_F16).
@@ -144,10 +144,12 @@ __device__ __forceinline__ void reduce_rows(const GemmArgs& a, const int (&m)[R]
                 g[r][e] = (float)gh[e] + db[e];
             }
     }
-    for (int z0 = 0; z0 < a.splits; z0 += 4) {
-        float4 p0[R][4], p1[R][4], q0[GG ? R : 1][4], q1[GG ? R : 1][4];
+    // splits per round: 8 for one plain row (16 float4 in flight), else 4
+    constexpr int U = (R == 1 && !GG) ? 8 : 4;
+    for (int z0 = 0; z0 < a.splits; z0 += U) {
+        float4 p0[R][U], p1[R][U], q0[GG ? R : 1][U], q1[GG ? R : 1][U];
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
+        for (int u = 0; u < U; ++u)
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const float* p = a.partial + min(z0 + u, a.splits - 1) * mn + (int64_t)m[r] * a.N + n;
@@ -159,7 +161,7 @@ __device__ __forceinline__ void reduce_rows(const GemmArgs& a, const int (&m)[R]
                 }
             }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < U; ++u) {
             const bool use = z0 + u < a.splits;
 #pragma unroll
             for (int r = 0; r < R; ++r) {
@@ -259,7 +261,9 @@ __global__ void splitk_reduce_kernel(GemmArgs a) {
     if (idx >= (int64_t)a.M * cpr) return;
     const int m[1] = {(int)(idx / cpr)};
     uint4 o[1];
-    reduce_rows<1, true>(a, m, 1u, (int)(idx - (int64_t)m[0] * cpr) * 8, o);
+    const int nout = (int)(idx - (int64_t)m[0] * cpr) * 8;
+    if (a.geglu) reduce_rows<1, true>(a, m, 1u, nout, o);
+    else reduce_rows<1, false>(a, m, 1u, nout, o);
 }
 
 // Main loop: NS-stage LDS ring fed by global_load_lds_dwordx4 (direct to LDS, no
