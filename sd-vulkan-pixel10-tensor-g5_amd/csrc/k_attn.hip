@@ -447,8 +447,10 @@ static void launch_cfg(const AttnArgs& a, hipStream_t s) {
     char name[48];
     // shared K/V tiles where there are enough query waves, or half as many with long
     // key sequences (the key-split kernel re-reads K/V per wave); two waves per block
-    // when four would leave < 512 blocks
-    if (qwaves >= 1024 || (qwaves >= 512 && a.Sk >= 512)) {
+    // when four would leave < 512 blocks.  Short key sequences (cross-attention over
+    // the 77 context tokens) go to the key-split kernel: staging a few K/V tiles per
+    // block costs more than each wave reading them.
+    if ((qwaves >= 1024 && a.Sk > 128) || (qwaves >= 512 && a.Sk >= 512)) {
         const int nw = ((a.Sq + 127) / 128) * bh >= 512 ? 4 : 2;
         snprintf(name, sizeof name, "attn_kernel<%d,%d,%d,%d>", KS, MTD, nw, (int)LSUM);
         const dim3 grid((a.Sq + nw * 32 - 1) / (nw * 32), a.heads, a.B);
