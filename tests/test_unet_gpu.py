@@ -111,9 +111,9 @@ def test_forward_affine_small():
 
 def test_forward_b3_24(unet_engine, oracle_weights):
     """Odd batch and a latent whose levels (576, 144, 36, 9 pixels per image) are not
-    multiples of the GEMM row tiles: 128-row tiles straddle two images at the first two
-    levels (GroupNorm statistics from the GEMM epilogues, two images per tile), and the
-    6x6 / 3x3 levels take the GroupNorm path that computes its own statistics."""
+    multiples of the GEMM row tiles: 128-row tiles straddle two images at the first
+    level (GroupNorm statistics from the GEMM epilogues, two images per tile), and the
+    smaller levels take the GroupNorm path that computes its own statistics."""
     lat, temb, ctx = inputs(3, 24, 24, seed=17)
     say("forward B=3 24x24")
     got = unet_engine.forward(lat, temb, ctx)
