@@ -300,8 +300,10 @@ struct SplitSmem {
 // One block = one group of 32 queries of one (image, head); wave w handles key
 // tiles w, w+NSPLIT, ...  K fragments come straight from global memory (each lane
 // reads 16 contiguous bytes of one key row); V goes through a per-wave transposed
-// LDS tile.  Within a wave LDS operations complete in order, so the per-wave tile
-// needs no block barrier; one barrier separates the key loop from the merge.
+// LDS tile (4 keys of one dim per 8-byte store).  A wave's next tile is loaded into
+// registers while the current one is computed.  Within a wave LDS operations
+// complete in order, so the per-wave tile needs no block barrier; one barrier
+// separates the key loop from the merge.
 template <int KS, int MTD, int NSPLIT, bool LSUM>
 __global__ __launch_bounds__(NSPLIT * 64) void attn_split_kernel(AttnArgs a) {
     constexpr int NTH = NSPLIT * 64;
@@ -337,10 +339,12 @@ __global__ __launch_bounds__(NSPLIT * 64) void attn_split_kernel(AttnArgs a) {
 
     const f16* kbase = a.k + (int64_t)b * a.Sk * a.ldk + (int64_t)h * d;
     const f16* vbase = a.v + (int64_t)b * a.Sk * a.ldv + (int64_t)h * d;
-    constexpr int MAXCH = (KTS * KS * 2 + 63) / 64;  // V chunks per lane per tile
-    const int nchunk = KTS * dch;
+    // V: one unit = the same 8 dims of 4 consecutive keys per lane, so that the
+    // transposed store to V^T [dim][key] is 8 ds_write_b64 (4 keys of one dim each)
+    constexpr int MAXU = (KTS / 4 * KS * 2 + 63) / 64;  // >= (KTS/4)*(d/8)/64
+    const int nunit = KTS / 4 * dch;
     half8 kf[KS];
-    uint4 rv[MAXCH];
+    uint4 rv[MAXU][4];
 
     auto load = [&](int kb) {
         const int key = kb + key_perm(lrow);
@@ -352,33 +356,48 @@ __global__ __launch_bounds__(NSPLIT * 64) void attn_split_kernel(AttnArgs a) {
             kf[ks] = v;
         }
 #pragma unroll
-        for (int i = 0; i < MAXCH; ++i) {
-            const int cidx = lane + i * 64;
-            uint4 vv = make_uint4(0, 0, 0, 0);
-            if (cidx < nchunk) {
-                const int kk = cidx / dch, dc = cidx - kk * dch;
-                if (kb + kk < a.Sk) vv = *(const uint4*)(vbase + (int64_t)(kb + kk) * a.ldv + dc * 8);
+        for (int i = 0; i < MAXU; ++i) {
+            const int u = lane + i * 64;
+            const int kq = u / dch, dc = u - kq * dch;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int key = kb + 4 * kq + j;
+                uint4 vv = make_uint4(0, 0, 0, 0);
+                if (u < nunit && key < a.Sk) vv = *(const uint4*)(vbase + (int64_t)key * a.ldv + dc * 8);
+                rv[i][j] = vv;
             }
-            rv[i] = vv;
         }
     };
     auto store_v = [&]() {
 #pragma unroll
-        for (int i = 0; i < MAXCH; ++i) {
-            const int cidx = lane + i * 64;
-            if (cidx < nchunk) {
-                const int kk = cidx / dch, dc = cidx - kk * dch;
-                const f16* vh = (const f16*)&rv[i];
+        for (int i = 0; i < MAXU; ++i) {
+            const int u = lane + i * 64;
+            if (u < nunit) {
+                const int kq = u / dch, c8 = (u - kq * dch) * 8, key = 4 * kq;
+                const uint32_t* w0 = (const uint32_t*)&rv[i][0];
+                const uint32_t* w1 = (const uint32_t*)&rv[i][1];
+                const uint32_t* w2 = (const uint32_t*)&rv[i][2];
+                const uint32_t* w3 = (const uint32_t*)&rv[i][3];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) vt[(dc * 8 + e) * VSTRS + kk] = vh[e];
+                for (int e2 = 0; e2 < 4; ++e2) {
+                    // dims 2*e2 (low halves) and 2*e2+1 (high halves) of the 4 keys
+                    const uint32_t lo01 = __builtin_amdgcn_perm(w1[e2], w0[e2], 0x05040100u);
+                    const uint32_t lo23 = __builtin_amdgcn_perm(w3[e2], w2[e2], 0x05040100u);
+                    const uint32_t hi01 = __builtin_amdgcn_perm(w1[e2], w0[e2], 0x07060302u);
+                    const uint32_t hi23 = __builtin_amdgcn_perm(w3[e2], w2[e2], 0x07060302u);
+                    *(uint2*)&vt[(c8 + 2 * e2) * VSTRS + key] = make_uint2(lo01, lo23);
+                    *(uint2*)&vt[(c8 + 2 * e2 + 1) * VSTRS + key] = make_uint2(hi01, hi23);
+                }
             }
         }
     };
 
+    // Each wave's tiles: the next tile's K and V are loaded into registers while the
+    // current one's softmax and PV run.
     const int ntile = (a.Sk + KTS - 1) / KTS;
+    if (wave < ntile) load(wave * KTS);
     for (int it = wave; it < ntile; it += NSPLIT) {
         const int kb = it * KTS;
-        load(kb);
         store_v();
         __builtin_amdgcn_wave_barrier();
         floatx16 s[1];
@@ -386,6 +405,7 @@ __global__ __launch_bounds__(NSPLIT * 64) void attn_split_kernel(AttnArgs a) {
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
             s[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[ks], qf[ks], s[0], 0, 0, 0);
+        if (it + NSPLIT < ntile) load(kb + NSPLIT * KTS);
         softmax_pv<1, MTD, LSUM>(s, min(KTS, a.Sk - kb), c, m_run, l_run, o, vt, VSTRS, hl, lrow, lk);
         __builtin_amdgcn_wave_barrier();
     }
@@ -445,12 +465,12 @@ static void launch_cfg(const AttnArgs& a, hipStream_t s) {
     const double flops = 4.0 * bh * a.Sq * a.Sk * a.d;
     const double bytes = 2.0 * bh * a.d * (2.0 * a.Sq + 2.0 * a.Sk);
     char name[48];
-    // shared K/V tiles where there are enough query waves, or half as many with long
-    // key sequences (the key-split kernel re-reads K/V per wave); two waves per block
-    // when four would leave < 512 blocks.  Short key sequences (cross-attention over
-    // the 77 context tokens) go to the key-split kernel: staging a few K/V tiles per
-    // block costs more than each wave reading them.
-    if ((qwaves >= 1024 && a.Sk > 128) || (qwaves >= 512 && a.Sk >= 512)) {
+    // shared K/V tiles where there are enough query waves to fill the chip (the
+    // key-split kernel re-reads K/V per wave); two waves per block when four would
+    // leave < 512 blocks.  Fewer query waves (e.g. 1024 queries x 16 heads), and short
+    // key sequences (cross-attention over the 77 context tokens), go to the key-split
+    // kernel: its extra waves, or not staging a few K/V tiles per block, win.
+    if (qwaves >= 1024 && a.Sk > 128) {
         const int nw = ((a.Sq + 127) / 128) * bh >= 512 ? 4 : 2;
         snprintf(name, sizeof name, "attn_kernel<%d,%d,%d,%d>", KS, MTD, nw, (int)LSUM);
         const dim3 grid((a.Sq + nw * 32 - 1) / (nw * 32), a.heads, a.B);
