@@ -23,6 +23,8 @@
 // exact two-pass mean / variance in registers.
 #include "sdu_internal.h"
 
+#include <cstdio>
+
 namespace sdu {
 
 static constexpr int GN_THREADS = 256;
@@ -276,46 +278,64 @@ __device__ __forceinline__ double gnf_block_sum(float v, double* red) {
     return t;
 }
 
-// One block per (group, image).  Thread t owns channel pair t % (cpg/2) of the group
-// and pixels t / (cpg/2) + k*P (P = pixels per sweep of the block), k < EP: each
-// load / store is one 4-byte pair at a fixed stride, and pairs never straddle the
-// concat split (C1 and C/G are even).
-template <int EP>
+// One block per (group, image).  Thread t owns VW consecutive channels (vector
+// t % (cpg/VW) of the group) and pixels t / (cpg/VW) + k*P (P = pixels per sweep of the
+// block), k < EP: each load / store is one VW*2-byte vector at a fixed stride, and
+// vectors never straddle the concat split (C1 and C/G are multiples of VW).
+template <int VW>
+struct GnfVec;
+template <>
+struct GnfVec<2> {
+    typedef uint32_t T;
+    static __device__ T load(__amdgpu_buffer_rsrc_t rs, int off) { return __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0); }
+};
+template <>
+struct GnfVec<4> {
+    typedef uint2 T;
+    static __device__ T load(__amdgpu_buffer_rsrc_t rs, int off) {
+        return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0));
+    }
+};
+template <>
+struct GnfVec<8> {
+    typedef uint4 T;
+    static __device__ T load(__amdgpu_buffer_rsrc_t rs, int off) {
+        return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+    }
+};
+
+template <int EP, int VW>
 __global__ __launch_bounds__(GNF_THREADS) void gn_fused_kernel(const f16* x, const f16* x2, int C1, int C2,
                                                                const f16* gamma, const f16* beta, f16* y,
                                                                int B, int HW, int G, float eps, int silu) {
+    typedef typename GnfVec<VW>::T V;
     __shared__ double red[GNF_THREADS / 64];
-    const int C = C1 + C2, cpg = C / G, hpg = cpg / 2;
+    const int C = C1 + C2, cpg = C / G, vpg = cpg / VW;
     const int g = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-    const int P = GNF_THREADS / hpg;
-    const int cp = tid % hpg, pp0 = tid / hpg;
+    const int P = GNF_THREADS / vpg;
+    const int cv = tid % vpg, pp0 = tid / vpg;
     const bool act = pp0 < P;
     const int pp = act ? pp0 : P - 1;
-    const int c = g * cpg + 2 * cp;
+    const int c = g * cpg + VW * cv;
     // All loads are issued before any is used, with 32-bit byte offsets into the
     // source; pixels past HW reload pixel HW-1 and are not accumulated.
-    uint32_t raw[EP];
-    if (c < C1) {
-        const __amdgpu_buffer_rsrc_t rs =
-            __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, B * HW * C1 * 2, 0x00020000);
-        const int vo = ((int)b * HW * C1 + c) * 2;
+    V raw[EP];
+    {
+        const bool first = c < C1;
+        const int Cs = first ? C1 : C2;
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(first ? x : x2), (short)0, B * HW * Cs * 2, 0x00020000);
+        const int vo = ((int)b * HW * Cs + (first ? c : c - C1)) * 2;
 #pragma unroll
-        for (int k = 0; k < EP; ++k)
-            raw[k] = __builtin_amdgcn_raw_buffer_load_b32(rs, vo + min(pp + k * P, HW - 1) * C1 * 2, 0, 0);
-    } else {
-        const __amdgpu_buffer_rsrc_t rs =
-            __builtin_amdgcn_make_buffer_rsrc((void*)x2, (short)0, B * HW * C2 * 2, 0x00020000);
-        const int vo = ((int)b * HW * C2 + (c - C1)) * 2;
-#pragma unroll
-        for (int k = 0; k < EP; ++k)
-            raw[k] = __builtin_amdgcn_raw_buffer_load_b32(rs, vo + min(pp + k * P, HW - 1) * C2 * 2, 0, 0);
+        for (int k = 0; k < EP; ++k) raw[k] = GnfVec<VW>::load(rs, vo + min(pp + k * P, HW - 1) * Cs * 2);
     }
     float s = 0.f;
 #pragma unroll
     for (int k = 0; k < EP; ++k) {
         if (act && pp + k * P < HW) {
             const f16* h = (const f16*)&raw[k];
-            s += (float)h[0] + (float)h[1];
+#pragma unroll
+            for (int e = 0; e < VW; ++e) s += (float)h[e];
         }
     }
     const double n = (double)HW * cpg;
@@ -326,15 +346,18 @@ __global__ __launch_bounds__(GNF_THREADS) void gn_fused_kernel(const f16* x, con
     for (int k = 0; k < EP; ++k) {
         if (act && pp + k * P < HW) {
             const f16* h = (const f16*)&raw[k];
-            const float d0 = (float)h[0] - mf, d1 = (float)h[1] - mf;
-            ss += d0 * d0 + d1 * d1;
+#pragma unroll
+            for (int e = 0; e < VW; ++e) {
+                const float dv = (float)h[e] - mf;
+                ss += dv * dv;
+            }
         }
     }
     const double var = gnf_block_sum(ss, red) / n;
     const float rstd = (float)(1.0 / sqrt(var + (double)eps));
-    float sc[2], sh[2];
+    float sc[VW], sh[VW];
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
+    for (int e = 0; e < VW; ++e) {
         sc[e] = rstd * (float)gamma[c + e];
         sh[e] = (float)beta[c + e] - mf * sc[e];
     }
@@ -344,15 +367,15 @@ __global__ __launch_bounds__(GNF_THREADS) void gn_fused_kernel(const f16* x, con
         const int p = pp + k * P;
         if (!act || p >= HW) continue;
         const f16* h = (const f16*)&raw[k];
-        uint32_t o;
+        V o;
         f16* oh = (f16*)&o;
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
+        for (int e = 0; e < VW; ++e) {
             float z = (float)h[e] * sc[e] + sh[e];
             if (silu) z = silu_f(z);
             oh[e] = (f16)z;
         }
-        *(uint32_t*)(dst + ((int64_t)b * HW + p) * C) = o;
+        *(V*)(dst + ((int64_t)b * HW + p) * C) = o;
     }
 }
 
@@ -373,22 +396,32 @@ hipError_t groupnorm_launch(const f16* x, const f16* x2, int C1, int C2, const f
         return hipErrorInvalidValue;
     const double xbytes = 2.0 * B * HW * C;
     const int cpg = C / G;
-    const int sweep = cpg % 2 == 0 ? GNF_THREADS / (cpg / 2) : 0;  // pixels per block sweep
+    // channels per thread: the widest vector that divides the group and the concat split
+    const int vw = (cpg % 8 == 0 && C1 % 8 == 0) ? 8 : (cpg % 4 == 0 && C1 % 4 == 0) ? 4 : 2;
+    const int sweep = cpg % 2 == 0 ? GNF_THREADS / (cpg / vw) : 0;  // pixels per block sweep
     const int nsweep = sweep ? (HW + sweep - 1) / sweep : 1 << 30;
     // one block per (image, group) wins while the slab is small; larger slabs stream
     // faster through the chunked two-kernel path, which spreads them over the chip
-    if (cpg % 2 == 0 && C1 % 2 == 0 && cpg / 2 <= GNF_THREADS && nsweep <= 32 &&
+    if (cpg % 2 == 0 && C1 % 2 == 0 && cpg / vw <= GNF_THREADS && nsweep <= 32 &&
         (int64_t)HW * cpg <= 32768 && 2 * (int64_t)B * HW * C < 0x7fffffff) {
         const int ep = nsweep <= 4 ? 4 : nsweep <= 8 ? 8 : nsweep <= 16 ? 16 : 32;
-        static const char* kNames[4] = {"gn_fused_kernel<4>", "gn_fused_kernel<8>", "gn_fused_kernel<16>",
-                                        "gn_fused_kernel<32>"};
-        const int vi = ep == 4 ? 0 : ep == 8 ? 1 : ep == 16 ? 2 : 3;
+        char name[40];
+        snprintf(name, sizeof name, "gn_fused_kernel<%d,%d>", ep, vw);
         const dim3 grid(G, B);
-        launch_timed(kNames[vi], 0.0, 2.0 * xbytes, [&] {
-            if (ep == 4) hipLaunchKernelGGL(gn_fused_kernel<4>, grid, dim3(GNF_THREADS), 0, s, x, x2, C1, C2, gamma, beta, y, B, HW, G, eps, silu);
-            else if (ep == 8) hipLaunchKernelGGL(gn_fused_kernel<8>, grid, dim3(GNF_THREADS), 0, s, x, x2, C1, C2, gamma, beta, y, B, HW, G, eps, silu);
-            else if (ep == 16) hipLaunchKernelGGL(gn_fused_kernel<16>, grid, dim3(GNF_THREADS), 0, s, x, x2, C1, C2, gamma, beta, y, B, HW, G, eps, silu);
-            else hipLaunchKernelGGL(gn_fused_kernel<32>, grid, dim3(GNF_THREADS), 0, s, x, x2, C1, C2, gamma, beta, y, B, HW, G, eps, silu);
+        launch_timed(name, 0.0, 2.0 * xbytes, [&] {
+#define GNF_LAUNCH(EPV, VWV)                                                                                 \
+    hipLaunchKernelGGL((gn_fused_kernel<EPV, VWV>), grid, dim3(GNF_THREADS), 0, s, x, x2, C1, C2, gamma, beta, y, \
+                       B, HW, G, eps, silu)
+#define GNF_VW(EPV)                      \
+    if (vw == 8) GNF_LAUNCH(EPV, 8);     \
+    else if (vw == 4) GNF_LAUNCH(EPV, 4); \
+    else GNF_LAUNCH(EPV, 2)
+            if (ep == 4) { GNF_VW(4); }
+            else if (ep == 8) { GNF_VW(8); }
+            else if (ep == 16) { GNF_VW(16); }
+            else { GNF_VW(32); }
+#undef GNF_VW
+#undef GNF_LAUNCH
         });
         return hipGetLastError();
     }
