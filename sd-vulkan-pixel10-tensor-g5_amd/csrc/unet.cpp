@@ -128,9 +128,9 @@ struct Act {
 // (then the GroupNorm that reads the output computes its own statistics).
 static void want_stats(Exec& E, GemmArgs& a, int HW) {
     const size_t n = (size_t)E.B * a.N * 2;
-    // up to 16x16 pixels the GroupNorm's own single-kernel statistics pass (one block
+    // up to 32x32 pixels the GroupNorm's own single-kernel statistics pass (one block
     // per group and image) costs less than the epilogue statistics and their apply
-    if (HW <= 256 || !gemm_stats_supported(HW) || E.st_next == nullptr || E.st_next + n > E.st_end) return;
+    if (HW <= 1024 || !gemm_stats_supported(HW) || E.st_next == nullptr || E.st_next + n > E.st_end) return;
     a.stats = E.st_next;
     a.stats_hw = HW;
     // a split GEMM whose partials go through the reduce launch leaves the statistics to
