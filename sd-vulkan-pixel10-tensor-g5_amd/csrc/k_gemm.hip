@@ -204,49 +204,6 @@ __device__ __forceinline__ void reduce_rows(const GemmArgs& a, const int (&m)[R]
     }
 }
 
-// Split-K reduce for outputs whose channel statistics are needed: block = 8 column
-// chunks (64 columns) x 32 row phases, each thread SR rows (rows of a block:
-// 32 * SR <= 64 <= stats_hw, so a block spans at most two images).
-template <int SR>
-__global__ __launch_bounds__(256) void splitk_reduce_stats_kernel(GemmArgs a) {
-    const int tid = threadIdx.x;
-    const int col0 = blockIdx.x * 64;
-    const int n = col0 + (tid & 7) * 8;
-    const int mb = blockIdx.y * 32 * SR;
-    const int b0 = mb / a.stats_hw;
-    float st[2][2][8];
-#pragma unroll
-    for (int sl = 0; sl < 2; ++sl)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) { st[sl][0][e] = 0.f; st[sl][1][e] = 0.f; }
-    if (n < a.N) {
-        int m[SR];
-        unsigned valid = 0;
-#pragma unroll
-        for (int j = 0; j < SR; ++j) {
-            const int mj = mb + (tid >> 3) + 32 * j;
-            if (mj < a.M) valid |= 1u << j;
-            m[j] = min(mj, a.M - 1);
-        }
-        uint4 o[SR];
-        reduce_rows<SR, false>(a, m, valid, n, o);
-#pragma unroll
-        for (int j = 0; j < SR; ++j) {
-            if (!(valid >> j & 1)) continue;
-            const f16* oh = (const f16*)&o[j];
-            const bool s1 = m[j] / a.stats_hw != b0;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float f = (float)oh[e];
-                if (s1) { st[1][0][e] += f; st[1][1][e] += f * f; }
-                else { st[0][0][e] += f; st[0][1][e] += f * f; }
-            }
-        }
-    }
-    __shared__ float red[256 * 32];
-    stats_flush(a, st, b0, min(a.M, mb + 32 * SR) - 1, col0, 8, red);
-}
-
 __global__ void splitk_reduce_kernel(GemmArgs a) {
     const int nout_cols = a.geglu ? a.N / 2 : a.N;
     const bool vec = a.out_mode != OUT_F32_NCHW && (a.N & 7) == 0;
@@ -828,7 +785,8 @@ void plan(const GemmArgs& a, int& ci, int& splits, int& kps, bool& fix) {
             bool fx = false;
             if (se > 1) {
                 const double part = (double)se * a.M * a.N * 8.0 / 20.0e12;
-                const double t_red = part + (a.stats ? 7.5e-6 : 5.5e-6);
+                // (with output statistics only the in-kernel sum: the reduce keeps none)
+                const double t_red = a.stats ? 1e30 : part + 5.5e-6;
                 const int rounds = ceil_div(se, fix_slots_per_round(g.mt, g.nt));
                 const double t_fix = tiles <= kMaxSplitTiles ? part + kFixBase + kFixRound * rounds : 1e30;
                 fx = t_fix < t_red;
@@ -841,13 +799,6 @@ void plan(const GemmArgs& a, int& ci, int& splits, int& kps, bool& fix) {
 }  // namespace
 
 bool gemm_stats_supported(int hw) { return stats_tile_ok(128, hw); }
-
-bool gemm_uses_reduce_kernel(const GemmArgs& a) {
-    int ci, splits, kps;
-    bool fix;
-    plan(a, ci, splits, kps, fix);
-    return splits > 1 && !fix;
-}
 
 const char* gemm_kernel_name(const GemmArgs& a) {
     int ci, splits, kps;
@@ -924,20 +875,9 @@ hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s) {
     if (e != hipSuccess || splits == 1 || fix) return e;
     const bool vec = a.out_mode != OUT_F32_NCHW && (a.N & 7) == 0;
     const int64_t total = (int64_t)a.M * (vec ? nout / 8 : nout);
-    if (a.stats) {
-        // two rows per thread when that still gives every CU a block
-        const bool two = (long)ceil_div(a.N, 64) * ceil_div(a.M, 64) >= 256;
-        const dim3 grid((unsigned)ceil_div(a.N, 64), (unsigned)ceil_div(a.M, two ? 64 : 32));
-        launch_timed(two ? "splitk_reduce_stats_kernel<2>" : "splitk_reduce_stats_kernel<1>", 0.0,
-                     part_bytes + out_bytes, [&] {
-            if (two) hipLaunchKernelGGL(splitk_reduce_stats_kernel<2>, grid, dim3(256), 0, s, a);
-            else hipLaunchKernelGGL(splitk_reduce_stats_kernel<1>, grid, dim3(256), 0, s, a);
-        });
-    } else {
-        launch_timed("splitk_reduce_kernel", 0.0, part_bytes + out_bytes, [&] {
-            hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, a);
-        });
-    }
+    launch_timed("splitk_reduce_kernel", 0.0, part_bytes + out_bytes, [&] {
+        hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, a);
+    });
     return hipGetLastError();
 }
 

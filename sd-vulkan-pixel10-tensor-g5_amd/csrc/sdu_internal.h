@@ -79,7 +79,8 @@ struct GemmArgs {
     // Optional per-channel statistics of the stored fp16 output, for a GroupNorm that
     // reads it: stats[b][n] += (sum, sum of squares) over the rows m of image
     // b = m / stats_hw.  Must be zero on entry.  fp16 output, no GEGLU, N % 8 == 0,
-    // stats_hw >= 64 and gemm_stats_supported(stats_hw).
+    // stats_hw >= 64 and gemm_stats_supported(stats_hw).  The planner then splits K
+    // only with the in-kernel sum (the reduce launch keeps no statistics).
     double* stats;
     int stats_hw;
 };
@@ -95,7 +96,6 @@ bool gemm_stats_supported(int hw);
 size_t gemm_counter_bytes();
 size_t gemm_workspace_bytes(const GemmArgs& a);
 const char* gemm_kernel_name(const GemmArgs& a);  // tile variant the launch will use
-bool gemm_uses_reduce_kernel(const GemmArgs& a);  // split K summed by a separate reduce launch
 hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s);
 
 // y[n] = act_out( sum_k act_in(x[k]) * W[n,k] + bias[n] ), fp32 in/out, W fp16 [N,K].

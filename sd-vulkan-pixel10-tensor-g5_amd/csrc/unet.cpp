@@ -133,12 +133,6 @@ static void want_stats(Exec& E, GemmArgs& a, int HW) {
     if (HW <= 1024 || !gemm_stats_supported(HW) || E.st_next == nullptr || E.st_next + n > E.st_end) return;
     a.stats = E.st_next;
     a.stats_hw = HW;
-    // a split GEMM whose partials go through the reduce launch leaves the statistics to
-    // the GroupNorm (its own statistics pass costs less than the reduce's atomics)
-    if (gemm_uses_reduce_kernel(a)) {
-        a.stats = nullptr;
-        return;
-    }
     E.st_next += n;
 }
 

@@ -111,14 +111,25 @@ def test_forward_affine_small():
 
 def test_forward_b3_24(unet_engine, oracle_weights):
     """Odd batch and a latent whose levels (576, 144, 36, 9 pixels per image) are not
-    multiples of the GEMM row tiles: 128-row tiles straddle two images at the first
-    level (GroupNorm statistics from the GEMM epilogues, two images per tile), and the
-    smaller levels take the GroupNorm path that computes its own statistics."""
+    multiples of the GEMM row tiles; every level's GroupNorms compute their own
+    statistics."""
     lat, temb, ctx = inputs(3, 24, 24, seed=17)
     say("forward B=3 24x24")
     got = unet_engine.forward(lat, temb, ctx)
     e = rel_err_l1(got, oracle_forward(oracle_weights, lat, temb, ctx))
     say(f"relErr B=3 24x24 = {e:.3e}")
+    assert e <= TOL
+
+
+def test_forward_b3_40(unet_engine, oracle_weights):
+    """Odd batch at 40x40: the first level (1600 pixels per image) takes GroupNorm
+    statistics from the GEMM epilogues, and its 128-row tiles straddle two images
+    (1600 = 12.5 x 128), so the epilogue's second-image slot is used."""
+    lat, temb, ctx = inputs(3, 40, 40, seed=18)
+    say("forward B=3 40x40")
+    got = unet_engine.forward(lat, temb, ctx)
+    e = rel_err_l1(got, oracle_forward(oracle_weights, lat, temb, ctx))
+    say(f"relErr B=3 40x40 = {e:.3e}")
     assert e <= TOL
 
 
