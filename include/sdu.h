@@ -63,8 +63,9 @@ int sdu_synchronize(sdu_ctx* ctx);
 /* Replace / read one UNet weight, given in its canonical diffusers layout
  * (conv [Co,Ci,kh,kw], Linear [out,in]) as float32 host data (rounded to fp16).
  * Synchronous; the next forward uses it.  Weights the engine keeps in a derived
- * form (a transformer's feed-forward output folded with its proj_out, a resnet's
- * conv2 with its 1x1 shortcut) are recomputed from their sources by this call. */
+ * form (a transformer's feed-forward output folded with its proj_out, its LayerNorm
+ * affines folded into the projections that read them, a resnet's conv2 with its 1x1
+ * shortcut) are recomputed from their sources by this call. */
 int sdu_set_weight(sdu_ctx* ctx, const char* name, const float* data, int64_t numel);
 int sdu_get_weight(sdu_ctx* ctx, const char* name, float* out, int64_t numel);
 /* Number of UNet parameters (859,520,964 for SD1.5) and of named tensors. */

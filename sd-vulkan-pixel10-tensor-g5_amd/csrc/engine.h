@@ -67,6 +67,13 @@ struct XfDesc {
     // feed-forward output and proj_out folded into one GEMM over [g | t] (fold_weights)
     f16* w_out = nullptr;  // [C, 5C] = [Wp.Wf | Wp]
     f16* b_out = nullptr;  // [C] = Wp.bf + bp
+    // LayerNorms norm1 / norm2 / norm3 folded into the GEMMs that read them (the QKV
+    // projection, the cross-attention query, the GEGLU projection): fp16 W' = W.diag(gamma),
+    // fp32 bias' = b + W.beta and column sums of W' (GemmArgs::ln_colsum)
+    f16* w_qkv = nullptr;  // [3C, C]
+    f16* w_q2 = nullptr;   // [C, C]
+    f16* w_ff = nullptr;   // [8C, C]
+    float *b_qkv = nullptr, *s_qkv = nullptr, *b_q2 = nullptr, *s_q2 = nullptr, *b_ff = nullptr, *s_ff = nullptr;
 };
 
 struct ProfAcc {

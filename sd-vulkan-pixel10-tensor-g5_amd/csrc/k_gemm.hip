@@ -12,7 +12,11 @@
 //     1x1 shortcut (:634) summed into its conv2.
 // Epilogue (fused; the reference runs these as separate AB/AB2/ADD/GEGLU passes):
 // + bias[n] + bias2[n] (fp32 time projection), GEGLU over interleaved a/b column
-// blocks, + residual, store fp16 / fp32 / fp32-NCHW.
+// blocks, + residual, store fp16 / fp32 / fp32-NCHW.  A LayerNorm (layernorm_f32.comp,
+// vk_engine.cpp:652, :658, :666) between two GEMMs runs inside them: the producer adds
+// each output row's sum and sum of squares into a row-statistics buffer, and the
+// consumer, reading the un-normalised rows as A, applies rstd * (acc - mean * colsum(W))
+// with the LayerNorm's affine folded into its W and bias.
 // Split-K, two ways: the last block of a tile to arrive sums the tile's fp32 partials
 // and runs the epilogue (few splits), or a reduce kernel does (many splits).
 #include "sdu_internal.h"
@@ -230,13 +234,22 @@ __global__ void splitk_reduce_kernel(GemmArgs a) {
 // 32x32x16 fragment reads (32 rows x 16 B per half-wave) are free of bank
 // conflicts.  Fragments are double-buffered in registers: the LDS reads of
 // k-step ks+1 are in flight during the MFMAs of k-step ks.
+// 8 consecutive fp32 values from 16-byte-aligned LDS
+__device__ __forceinline__ void ld8(const float* p, float (&v)[8]) {
+    const float4 x = *(const float4*)p, y = *(const float4*)(p + 4);
+    v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w; v[4] = y.x; v[5] = y.y; v[6] = y.z; v[7] = y.w;
+}
+
 template <int BKT>
 __device__ __forceinline__ int lds_swizzle(int row) {
     return BKT == 64 ? ((row >> 1) & 7) : ((row >> 2) & 3);
 }
 
+// Two blocks per CU (4 waves per SIMD) where the ring leaves LDS for two: the
+// register budget is then 128 VGPRs.
 template <int MT, int NT, int WM, int WN, int BKT, int NS, int AM>
-__global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
+__global__ __launch_bounds__(WM* WN * 64) __attribute__((amdgpu_waves_per_eu(MT == 256 ? 2 : 4)))
+void gemm_kernel(GemmArgs a) {
     constexpr int NW = WM * WN, NTH = NW * 64;
     constexpr int TMW = MT / WM, TNW = NT / WN;  // wave tile
     constexpr int FM = TMW / 32, FN = TNW / 32;   // 32x32 MFMA tiles per wave
@@ -246,6 +259,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
     constexpr int LPT = AI + BI;
     constexpr int STAGE = (MT + NT) * BKT;        // halves per ring stage
     constexpr int KS = BKT / 16;                  // MFMA k-steps per tile
+    constexpr bool DENSE = AM == A_DENSE;
     static_assert(AI * RPI * NW == MT && BI * RPI * NW == NT, "DMA split");
     static_assert(NS >= 2 && (NS - 2) * LPT < 64, "ring depth");
 
@@ -312,7 +326,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
         a_c[i] = (pchunk ^ lds_swizzle<BKT>(row)) * 8;
         const int m = min(m0 + row, a.M - 1);
         a_m[i] = m;
-        if (AM == A_DENSE) {
+        if (DENSE) {
             voA[i] = (uint32_t)((m * a.lda + a_c[i]) * 2);
             voA2[i] = a.A2 ? (uint32_t)((m * a.lda2 + a_c[i]) * 2) : 0u;
         } else {
@@ -338,7 +352,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
     }
     const __amdgpu_buffer_rsrc_t rsA = __builtin_amdgcn_make_buffer_rsrc(
         (void*)a.A, (short)0,
-        AM == A_DENSE ? a.M * a.lda * 2 : a.Bn * a.Hin * a.Win * a.Cin * 2, 0x00020000);
+        DENSE ? a.M * a.lda * 2 : a.Bn * a.Hin * a.Win * a.Cin * 2, 0x00020000);
     const __amdgpu_buffer_rsrc_t rsA2 = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(a.A2 ? a.A2 : a.A), (short)0, a.A2 ? a.M * a.lda2 * 2 : 0, 0x00020000);
     const __amdgpu_buffer_rsrc_t rsA3 = __builtin_amdgcn_make_buffer_rsrc(
@@ -360,7 +374,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
         const bool tail = k0 + BKT > kend;  // partial K tile
         f16* sA = smem + stage * STAGE;
         f16* sB = sA + MT * BKT;
-        if (AM == A_DENSE) {
+        if (DENSE) {
             const bool in1 = !a.A2 || k0 + BKT <= a.K1, in2 = a.A2 && k0 >= a.K1;
             if (!tail && in1) {
 #pragma unroll
@@ -458,6 +472,22 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
     for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = floatx16{};
+    // LayerNorm consumer: the PPT consecutive lanes of tile row t / PPT load its 64-column
+    // partials j = t % PPT, + PPT, ... (issued before the first K tiles, added after),
+    // and thread t < NT the column sum of tile column t
+    constexpr int PPT = NTH / MT, MAXP = 20 / PPT;  // lanes per row, partials per lane (K <= 1280)
+    const bool lnc = DENSE && a.ln_part != nullptr;
+    float2 ln_v[MAXP];
+    float ln_cs_t = 0.f;
+    if (lnc) {
+        const int mm = min(m0 + tid / PPT, a.M - 1), T = a.K >> 6;
+#pragma unroll
+        for (int i = 0; i < MAXP; ++i) {
+            const int j = tid % PPT + i * PPT;
+            ln_v[i] = j < T ? *(const float2*)(a.ln_part + ((int64_t)j * a.M + mm) * 2) : make_float2(0.f, 0.f);
+        }
+        if (tid < NT && n0 + tid < a.N) ln_cs_t = a.ln_colsum[n0 + tid];
+    }
 
     // fragment addressing: row (base + lrow), logical chunk 2*ks + (lane>>5);
     // every fragment base row is a multiple of 32, so the swizzle depends on lrow only
@@ -465,6 +495,11 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int p = 0; p < NS - 1; ++p)
         if (p < nk) issue(p, p);
+    float ln_s1 = 0.f, ln_s2 = 0.f;
+    if (lnc) {
+#pragma unroll
+        for (int i = 0; i < MAXP; ++i) { ln_s1 += ln_v[i].x; ln_s2 += ln_v[i].y; }
+    }
     for (int kt = 0; kt < nk; ++kt) {
         // tile kt must have landed; the tiles issued after it may still be in flight
         const int ahead = min(NS - 2, nk - 1 - kt);
@@ -511,6 +546,20 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
 
     // ---- epilogue
     const int col_l = lane & 31, rq = (lane >> 5) * 4;
+    float2 ln_rs = make_float2(1.f, 0.f);  // (rstd, -mean * rstd) of row tid / PPT
+    if (lnc) {
+        // the row's PPT lanes add their partials
+#pragma unroll
+        for (int off = 1; off < PPT; off <<= 1) {
+            ln_s1 += __shfl_xor(ln_s1, off);
+            ln_s2 += __shfl_xor(ln_s2, off);
+        }
+        // one-pass statistics as the reference's layernorm_f32.comp (clamped at 0)
+        const float inv_k = 1.0f / (float)a.K;
+        const float mean = ln_s1 * inv_k;
+        const float rstd = rsqrtf(fmaxf(ln_s2 * inv_k - mean * mean, 0.f) + a.ln_eps);
+        ln_rs = make_float2(rstd, -mean * rstd);
+    }
     if (a.partial && !a.fixup) {
         // split K, reduce kernel: fp32 partial [split][M][N]
         float* P = a.partial + (int64_t)blockIdx.z * a.M * a.N;
@@ -614,6 +663,12 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
     static_assert(PR * CST * 4 <= NS * STAGE * 2, "C pass fits the operand LDS");
     static_assert(NTH * 32 * 4 <= NS * STAGE * 2, "statistics flush fits the operand LDS");
     float* Cs = (float*)smem;
+    // LayerNorm consumer tables after the C pass area: (rstd, -mean * rstd) per tile
+    // row, column sums of the tile's columns (written after the first pass barrier)
+    constexpr int TBL = PR * CST;
+    static_assert((TBL + 2 * MT + NT) * 4 <= NS * STAGE * 2, "LayerNorm tables fit the operand LDS");
+    float2* const ln_rt = (float2*)(Cs + TBL);
+    float* const ln_cs = Cs + TBL + 2 * MT;
     float badd[8], gadd[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) { badd[e] = 0.f; gadd[e] = 0.f; }
@@ -648,9 +703,21 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
     for (int sl = 0; sl < 2; ++sl)
 #pragma unroll
         for (int e = 0; e < 8; ++e) { st[sl][0][e] = 0.f; st[sl][1][e] = 0.f; }
+    // per-row output statistics (LayerNorm of the consumer): this thread's 8 columns
+    // of each of its rows
+    const bool do_rs = a.row_part != nullptr && !narrow;
+    float rsum[FM][MAXR], rsq[FM][MAXR];
+#pragma unroll
+    for (int ip = 0; ip < FM; ++ip)
+#pragma unroll
+        for (int k = 0; k < MAXR; ++k) { rsum[ip][k] = 0.f; rsq[ip][k] = 0.f; }
 #pragma unroll
     for (int ip = 0; ip < FM; ++ip) {
         __syncthreads();
+        if (lnc && ip == 0) {
+            if (tid % PPT == 0) ln_rt[tid / PPT] = ln_rs;
+            if (tid < NT) ln_cs[tid] = ln_cs_t;
+        }
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
@@ -679,11 +746,33 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
             const int sr = r0 + k * rstep;
             const int m = m0 + (sr >> 5) * TMW + ip * 32 + (sr & 31);
             if (sr >= PR || m >= a.M) continue;
+            // the row's 8 (GEGLU: 2 x 8) staged values as 16-byte LDS reads (rows are
+            // CST = NT + 4 floats, tc a multiple of 8: 16-byte aligned)
+            // (LayerNorm consumer: rstd * (acc - mean * colsum) + bias)
+            const float* crow = Cs + sr * CST + tc;
+            float2 lt = make_float2(1.f, 0.f);
+            if (lnc) lt = ln_rt[(sr >> 5) * TMW + ip * 32 + (sr & 31)];
             float v[8];
+            ld8(crow, v);
+            if (lnc) {
+                float sn[8];
+                ld8(ln_cs + tc, sn);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                v[e] = Cs[sr * CST + tc + e] + badd[e];
-                if (a.geglu) v[e] *= gelu_erf(Cs[sr * CST + tc + 32 + e] + gadd[e]);
+                for (int e = 0; e < 8; ++e) v[e] = fmaf(lt.x, v[e], lt.y * sn[e]);
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] += badd[e];
+            if (a.geglu) {
+                float g[8];
+                ld8(crow + 32, g);
+                if (lnc) {
+                    float sn[8];
+                    ld8(ln_cs + tc + 32, sn);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) g[e] = fmaf(lt.x, g[e], lt.y * sn[e]);
+                }
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] *= gelu_erf(g[e] + gadd[e]);
             }
             if (a.res) {
                 const f16* rh = (const f16*)&rres[ip][k];
@@ -696,6 +785,14 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) oh[e] = (f16)v[e];
                 *(uint4*)((f16*)a.C + (int64_t)m * a.ldc + nout) = o;
+                if (do_rs) {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const float f = (float)oh[e];
+                        rsum[ip][k] += f;
+                        rsq[ip][k] += f * f;
+                    }
+                }
                 if (do_st) {
                     const bool s1 = m / a.stats_hw != st_b0;
 #pragma unroll
@@ -713,6 +810,25 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs a) {
         }
     }
     if (do_st) stats_flush(a, st, st_b0, min(a.M, m0 + MT) - 1, n0, cpr, (float*)smem);
+    if (do_rs) {
+        // the cpr threads of a row are consecutive lanes, each 8 of them one 64-column
+        // group: add their partial sums; the first of the 8 stores the group's partial
+#pragma unroll
+        for (int ip = 0; ip < FM; ++ip)
+#pragma unroll
+            for (int k = 0; k < MAXR; ++k) {
+                float s1 = rsum[ip][k], s2 = rsq[ip][k];
+#pragma unroll
+                for (int off = 1; off < 8; off <<= 1) {
+                    s1 += __shfl_xor(s1, off);
+                    s2 += __shfl_xor(s2, off);
+                }
+                const int sr = r0 + k * rstep;
+                const int m = m0 + (sr >> 5) * TMW + ip * 32 + (sr & 31);
+                if ((oc & 63) == 0 && sr < PR && m < a.M && n < a.N)
+                    *(float2*)(a.row_part + ((int64_t)(n >> 6) * a.M + m) * 2) = make_float2(s1, s2);
+            }
+    }
 }
 
 namespace {
@@ -786,7 +902,7 @@ void plan(const GemmArgs& a, int& ci, int& splits, int& kps, bool& fix) {
             if (se > 1) {
                 const double part = (double)se * a.M * a.N * 8.0 / 20.0e12;
                 // (with output statistics only the in-kernel sum: the reduce keeps none)
-                const double t_red = a.stats ? 1e30 : part + 5.5e-6;
+                const double t_red = (a.stats || a.row_part || a.ln_part) ? 1e30 : part + 5.5e-6;
                 const int rounds = ceil_div(se, fix_slots_per_round(g.mt, g.nt));
                 const double t_fix = tiles <= kMaxSplitTiles ? part + kFixBase + kFixRound * rounds : 1e30;
                 fx = t_fix < t_red;
@@ -833,6 +949,12 @@ hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s) {
     if (a.A2 == nullptr) a.K1 = a.K;
     if (a.A3 == nullptr) a.K2 = a.K;
     if (a.A3 && (a.amode != A_CONV3 || !a.A2)) return hipErrorInvalidValue;
+    // (a consumer thread sums up to 10 row partials; 2 or 4 threads per tile row)
+    if (a.ln_part && (a.amode != A_DENSE || a.A2 || !a.ln_colsum || a.out_mode != OUT_F16 || (a.N & 7) ||
+                      (a.K & 63) || a.K > 1280 || !(a.ln_eps > 0.f) || (splits > 1 && !fix)))
+        return hipErrorInvalidValue;
+    if (a.row_part && (a.out_mode != OUT_F16 || a.geglu || (a.N & 63) || (splits > 1 && !fix)))
+        return hipErrorInvalidValue;
     if (a.amode == A_CONV3 && a.A2 &&
         (a.K1 != 9 * a.Cin || a.K1 % 64 || a.K2 % 64 || a.K % 64 || a.K2 <= a.K1 || a.K <= a.K1 ||
          (a.A3 && a.K2 >= a.K) || a.stride != 1 || a.upsample || a.Ho != a.Hin || a.Wo != a.Win ||

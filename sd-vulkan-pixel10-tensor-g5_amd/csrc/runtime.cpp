@@ -177,6 +177,30 @@ int build_inventory(Ctx& c) {
 
     // ---- pool layout (element offsets, 128-element = 256-byte aligned)
     auto align = [](int64_t n) { return (n + 127) & ~(int64_t)127; };
+    // a transformer's folded weights, in this order: w_out, b_out, w_qkv, w_q2, w_ff
+    // (fp16), then b_qkv, s_qkv, b_q2, s_q2, b_ff, s_ff (fp32, two halves each)
+    auto xf_fold = [&](int64_t ch, XfDesc* xd, f16* base) {
+        int64_t o = 0;
+        auto h = [&](int64_t n) { f16* p = base ? base + o : nullptr; o += align(n); return p; };
+        auto f = [&](int64_t n) { return (float*)h(2 * n); };
+        f16* w_out = h(5 * ch * ch);
+        f16* b_out = h(ch);
+        f16* w_qkv = h(3 * ch * ch);
+        f16* w_q2 = h(ch * ch);
+        f16* w_ff = h(8 * ch * ch);
+        float* b_qkv = f(3 * ch);
+        float* s_qkv = f(3 * ch);
+        float* b_q2 = f(ch);
+        float* s_q2 = f(ch);
+        float* b_ff = f(8 * ch);
+        float* s_ff = f(8 * ch);
+        if (xd) {
+            xd->w_out = w_out; xd->b_out = b_out; xd->w_qkv = w_qkv; xd->w_q2 = w_q2; xd->w_ff = w_ff;
+            xd->b_qkv = b_qkv; xd->s_qkv = s_qkv; xd->b_q2 = b_q2; xd->s_q2 = s_q2; xd->b_ff = b_ff;
+            xd->s_ff = s_ff;
+        }
+        return o;
+    };
     int64_t top = 0;
     const int64_t off_tproj_w = top; top += align((int64_t)c.tproj_total * kTembDim);
     const int64_t off_tproj_b = top; top += align(c.tproj_total);
@@ -191,7 +215,7 @@ int build_inventory(Ctx& c) {
     for (size_t i = 0; i < c.xfs.size(); ++i) {
         const int64_t ch = c.xfs[i].c;
         off_fold[i] = top;
-        top += align(5 * ch * ch) + align(ch);
+        top += xf_fold(ch, nullptr, nullptr);
     }
     for (size_t i = 0; i < c.resnets.size(); ++i) {
         const ResDesc& rd = c.resnets[i];
@@ -226,8 +250,7 @@ int build_inventory(Ctx& c) {
         const std::string b = xd.pf + ".transformer_blocks.0";
         c.weights[c.widx[b + ".attn2.to_k.weight"]].dev = c.w_kv + (int64_t)xd.kv_off * kCtxDim;
         c.weights[c.widx[b + ".attn2.to_v.weight"]].dev = c.w_kv + (int64_t)(xd.kv_off + xd.c) * kCtxDim;
-        xd.w_out = P + off_fold[i];
-        xd.b_out = xd.w_out + align(5 * (int64_t)xd.c * xd.c);
+        xf_fold(xd.c, &xd, P + off_fold[i]);
     }
     return SDU_OK;
 }
@@ -244,9 +267,21 @@ int fold_weights(Ctx& c, const std::string& name) {
     for (const XfDesc& xd : c.xfs) {
         if (!name.empty() && name.compare(0, xd.pf.size() + 1, xd.pf + ".") != 0) continue;
         const std::string b = xd.pf + ".transformer_blocks.0";
+        const int C = xd.c;
         hipError_t e = fold_ffout_launch(c.wd(xd.pf + ".proj_out.weight"), c.wd(xd.pf + ".proj_out.bias"),
                                          c.wd(b + ".ff.net.2.weight"), c.wd(b + ".ff.net.2.bias"), xd.w_out,
-                                         xd.b_out, xd.c, c.stream);
+                                         xd.b_out, C, c.stream);
+        // to_q, to_k, to_v are consecutive [C, C] blocks of the pool: one [3C, C] weight
+        if (e == hipSuccess)
+            e = fold_ln_launch(c.wd(b + ".attn1.to_q.weight"), nullptr, c.wd(b + ".norm1.weight"),
+                               c.wd(b + ".norm1.bias"), xd.w_qkv, xd.b_qkv, xd.s_qkv, 3 * C, C, c.stream);
+        if (e == hipSuccess)
+            e = fold_ln_launch(c.wd(b + ".attn2.to_q.weight"), nullptr, c.wd(b + ".norm2.weight"),
+                               c.wd(b + ".norm2.bias"), xd.w_q2, xd.b_q2, xd.s_q2, C, C, c.stream);
+        if (e == hipSuccess)
+            e = fold_ln_launch(c.wd(b + ".ff.net.0.proj.weight"), c.wd(b + ".ff.net.0.proj.bias"),
+                               c.wd(b + ".norm3.weight"), c.wd(b + ".norm3.bias"), xd.w_ff, xd.b_ff, xd.s_ff,
+                               8 * C, C, c.stream);
         if (e != hipSuccess) return set_err(&c, SDU_ERR_HIP, std::string("weight fold: ") + hipGetErrorString(e));
     }
     hipError_t e = hipStreamSynchronize(c.stream);

@@ -83,6 +83,19 @@ struct GemmArgs {
     // only with the in-kernel sum (the reduce launch keeps no statistics).
     double* stats;
     int stats_hw;
+    // Optional LayerNorm between two GEMMs.  Producer: row_part[n / 64][m] = (sum, sum of
+    // squares) of row m of the stored fp16 output over columns [n, n + 64) (fp32
+    // [N / 64][M][2], every entry written; fp16 output, no GEGLU, N % 64 == 0).
+    // Consumer (dense A from one source, fp16 output, N % 8 == 0, K % 64 == 0,
+    // K <= 1280): ln_part holds those partials of A ([K / 64][M][2]), and the epilogue
+    // computes
+    //   C[m, n] = rstd_m * (sum_k A[m, k] W[n, k] - mean_m * ln_colsum[n]) + bias...
+    // (eps ln_eps), the LayerNorm's affine folded into W and the bias (fold_ln_launch).
+    // With either, the planner splits K only with the in-kernel sum.
+    float* row_part;
+    const float* ln_part;
+    const float* ln_colsum;  // [N]: sum_k W[n, k] of the fp16 W
+    float ln_eps;
 };
 
 // Whether a GEMM can produce output statistics for images of `hw` rows (some tile
@@ -172,6 +185,11 @@ hipError_t gen_launch(f16* dst, const GenDesc& g, hipStream_t s);
 // for proj_out (Wp [C, C], bp) after the feed-forward output (Wf [C, 4C], bf).  C % 16 == 0.
 hipError_t fold_ffout_launch(const f16* Wp, const f16* bp, const f16* Wf, const f16* bf, f16* wcat, f16* bcat,
                              int C, hipStream_t s);
+// LayerNorm affine folded into the Linear that reads it (init time): Wf[n, k] =
+// gamma[k] W[n, k] (fp16), bf[n] = b[n] + sum_k beta[k] W[n, k] (b may be null),
+// sf[n] = sum_k Wf[n, k] (GemmArgs::ln_colsum).
+hipError_t fold_ln_launch(const f16* W, const f16* b, const f16* gamma, const f16* beta, f16* Wf, float* bf,
+                          float* sf, int N, int K, hipStream_t s);
 // Resnet shortcut fold (init time): wcat [Co, 9 Ci2 + Cs] = [conv2 (OHWI) | shortcut],
 // bcat = b2 + bs, for conv2 over Ci2 channels and a 1x1 shortcut over Cs channels.
 hipError_t fold_shortcut_launch(const f16* w2, const f16* b2, const f16* ws, const f16* bs, f16* wcat, f16* bcat,

@@ -84,7 +84,7 @@ static void gemm(Exec& E, const char* cat, const GemmArgs& a) {
     const size_t ws = gemm_workspace_bytes(a);
     if (ws > E.gemm_ws_need) E.gemm_ws_need = ws;
     char shape[96];
-    snprintf(shape, sizeof shape, "%s M=%d N=%d K=%d geglu=%d", a.amode == A_CONV3 ? "conv3" : "dense",
+    snprintf(shape, sizeof shape, "%s M=%d N=%d K=%d geglu=%d", a.amode == A_CONV3 ? "conv3" : a.ln_colsum ? "dense_ln" : "dense",
              a.M, a.N, a.K, a.geglu);
     E.run(cat, [&] { return gemm_launch(a, E.gemm_ws, E.s); }, shape);
 }
@@ -152,10 +152,6 @@ static void groupnorm(Exec& E, Act x, Act x2, int C1, int C2, const f16* g, cons
     E.run(silu ? "groupnorm_silu" : "groupnorm", [&] {
         return groupnorm_launch(x.p, x2.p, C1, C2, g, b, y, E.B, HW, kGroups, kEps, silu, acc, E.s);
     }, shape);
-}
-
-static void layernorm(Exec& E, const f16* x, const f16* g, const f16* b, f16* y, int T, int C) {
-    E.run("layernorm", [&] { return layernorm_launch(x, g, b, y, T, C, kEps, E.s); });
 }
 
 static void attention(Exec& E, const char* cat, const f16* q, const f16* k, const f16* v, f16* o,
@@ -228,6 +224,10 @@ static Act transformer(Exec& E, const XfDesc& t, Act xa, int H, int Wd, const f1
     const std::string b = t.pf + ".transformer_blocks.0";
     f16* out = E.alloc<f16>((size_t)M * C);
     const size_t mk = E.ar->mark();
+    // 64-column partial row sums / sums of squares of the token stream tt before norm1,
+    // norm2, norm3 (GemmArgs::row_part)
+    const size_t np = (size_t)(C / 64) * M * 2;
+    float* rp = E.alloc<float>(3 * np);
     f16* g = E.alloc<f16>((size_t)M * C);
     groupnorm(E, xa, Act{nullptr, nullptr}, C, 0, W(E, t.pf + ".norm.weight"), W(E, t.pf + ".norm.bias"), g,
               HW, 0);
@@ -235,41 +235,51 @@ static Act transformer(Exec& E, const XfDesc& t, Act xa, int H, int Wd, const f1
     {
         GemmArgs a = dense_args(g, C, M, C, C, W(E, t.pf + ".proj_in.weight"), tt, C);
         a.bias = W(E, t.pf + ".proj_in.bias");
+        a.row_part = rp;
         gemm(E, "conv1x1", a);
     }
-    f16* h = E.alloc<f16>((size_t)M * C);
     f16* qkv = E.alloc<f16>((size_t)M * 3 * C);
     f16* at = E.alloc<f16>((size_t)M * C);
+    // Each LayerNorm (norm1, norm2, norm3) runs inside the GEMMs around it: the GEMM
+    // that writes the token stream tt keeps its row statistics, and the GEMM that
+    // reads it takes tt as A with the folded weight / bias / column sums (fold_weights).
+    auto ln_gemm = [&](f16* out, int N, int ldo, const f16* w, const float* bias, const float* colsum,
+                       const float* part) {
+        GemmArgs a = dense_args(tt, C, M, N, C, w, out, ldo);
+        a.bias2 = bias;
+        a.ln_part = part;
+        a.ln_colsum = colsum;
+        a.ln_eps = kEps;
+        return a;
+    };
     // self-attention
-    layernorm(E, tt, W(E, b + ".norm1.weight"), W(E, b + ".norm1.bias"), h, M, C);
-    gemm(E, "linear", dense_args(h, C, M, 3 * C, C, W(E, b + ".attn1.to_q.weight"), qkv, 3 * C));
+    gemm(E, "linear", ln_gemm(qkv, 3 * C, 3 * C, t.w_qkv, t.b_qkv, t.s_qkv, rp));
     attention(E, "attn_self", qkv, qkv + C, qkv + 2 * C, at, HW, HW, C, 3 * C, 3 * C, 3 * C);
     {
         GemmArgs a = dense_args(at, C, M, C, C, W(E, b + ".attn1.to_out.0.weight"), tt, C);
         a.bias = W(E, b + ".attn1.to_out.0.bias");
         a.res = tt; a.ldr = C;
+        a.row_part = rp + np;
         gemm(E, "linear", a);
     }
     // cross-attention: K/V of this block are columns [kv_off, kv_off + 2C) of kv
-    layernorm(E, tt, W(E, b + ".norm2.weight"), W(E, b + ".norm2.bias"), h, M, C);
-    gemm(E, "linear", dense_args(h, C, M, C, C, W(E, b + ".attn2.to_q.weight"), qkv, C));
+    gemm(E, "linear", ln_gemm(qkv, C, C, t.w_q2, t.b_q2, t.s_q2, rp + np));
     const int ldkv = E.c.kv_total;
     attention(E, "attn_cross", qkv, kv + t.kv_off, kv + t.kv_off + C, at, HW, L, C, C, ldkv, ldkv);
     {
         GemmArgs a = dense_args(at, C, M, C, C, W(E, b + ".attn2.to_out.0.weight"), tt, C);
         a.bias = W(E, b + ".attn2.to_out.0.bias");
         a.res = tt; a.ldr = C;
+        a.row_part = rp + 2 * np;
         gemm(E, "linear", a);
     }
     // GEGLU feed-forward: proj (+bias, GEGLU in the epilogue).  Its output projection
     // (+bias, +residual t) and proj_out (+bias, +residual x) are one GEMM over the
     // two-source A = [ff | t] with the folded weight [Wp.Wf | Wp] (fold_weights):
     // out = Wp.(t + Wf.ff + bf) + bp + x.
-    layernorm(E, tt, W(E, b + ".norm3.weight"), W(E, b + ".norm3.bias"), h, M, C);
     f16* ff = E.alloc<f16>((size_t)M * 4 * C);
     {
-        GemmArgs a = dense_args(h, C, M, 8 * C, C, W(E, b + ".ff.net.0.proj.weight"), ff, 4 * C);
-        a.bias = W(E, b + ".ff.net.0.proj.bias");
+        GemmArgs a = ln_gemm(ff, 8 * C, 4 * C, t.w_ff, t.b_ff, t.s_ff, rp + 2 * np);
         a.geglu = 1;
         gemm(E, "linear_geglu", a);
     }

@@ -178,6 +178,48 @@ def test_set_weight_refolds(unet_engine, oracle_weights):
             unet_engine.set_weight(n, v)
 
 
+def test_set_weight_refolds_layernorm(unet_engine, oracle_weights):
+    """The transformer LayerNorms (norm1 / norm2 / norm3) run inside the GEMMs that
+    read them (row statistics from the A tiles, affine folded into the weights).
+    Non-trivial scales and shifts and new projection weights, set through
+    sdu_set_weight, refold: the forward matches the oracle with the same weights, at
+    C = 320, 640 and 1280 (mid block: 16 tokens, rows past M in every tile)."""
+    blocks = ["up_blocks.3.attentions.2.transformer_blocks.0", "down_blocks.1.attentions.0.transformer_blocks.0",
+              "mid_block.attentions.0.transformer_blocks.0"]
+    sufs = ["norm1.weight", "norm1.bias", "norm2.weight", "norm2.bias", "norm3.weight", "norm3.bias",
+            "attn1.to_k.weight", "attn2.to_q.weight", "ff.net.0.proj.weight", "ff.net.0.proj.bias"]
+    specs = {p.name: p for p in Wt.param_specs()}
+    rng = np.random.default_rng(6)
+    p2 = dict(oracle_weights)
+    orig = {}
+    try:
+        for b in blocks:
+            for sfx in sufs:
+                n = b + "." + sfx
+                shape = specs[n].shape
+                if sfx.startswith("norm") and sfx.endswith(".weight"):
+                    v = 1.0 + 0.5 * rng.standard_normal(shape)
+                elif sfx.startswith("norm"):
+                    v = 0.5 * rng.standard_normal(shape)
+                else:
+                    v = 0.05 * rng.standard_normal(shape)
+                v = v.astype(np.float16).astype(np.float32)
+                orig[n] = unet_engine.get_weight(n, shape)
+                unet_engine.set_weight(n, v)
+                p2[n] = torch.from_numpy(v)
+        lat, temb, ctx = inputs(1, 32, 32, seed=18)
+        say("forward B=1 32x32 after set_weight on LayerNorm-folded sources")
+        got = unet_engine.forward(lat, temb, ctx)
+        e = rel_err_l1(got, oracle_forward(p2, lat, temb, ctx))
+        e_old = rel_err_l1(got, oracle_forward(oracle_weights, lat, temb, ctx))
+        say(f"relErr new weights = {e:.3e}, vs old weights = {e_old:.3e}")
+        assert e <= TOL
+        assert e_old > max(TOL, 5 * e)
+    finally:
+        for n, v in orig.items():
+            unet_engine.set_weight(n, v)
+
+
 def test_forward_b16_matches_pairs(unet_engine):
     """B=16 throughput batch: eight copies of one CFG pair must each reproduce the
     B=2 result (per-image independence of every kernel; split-K factors differ
