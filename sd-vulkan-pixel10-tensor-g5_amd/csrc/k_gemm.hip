@@ -29,9 +29,6 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ float gelu_erf(float x) {
-    return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));
-}
 
 // Final value for output element (m, output column nout) given the fp32 GEMM
 // results for column n (and its GEGLU gate partner).
@@ -69,13 +66,15 @@ __device__ __forceinline__ void wait_vmcnt_lgkm0() {
 }
 
 // Sum the per-thread column statistics of a block over the threads that own the same
-// 8 columns (thread t owns chunk t % cpr; chunk c covers columns col0 + 8c ..) through
+// 8 columns (thread t owns chunk t % CPR; chunk c covers columns col0 + 8c ..) through
 // LDS and add them to the per-(image, channel) fp64 statistics, one atomic per value,
-// the sums spread over all threads.  red must hold blockDim.x * 32 floats and be free
-// (the caller's last LDS use is complete after the first barrier here).
+// the sums spread over all threads (each one's NTH / CPR LDS reads issued together).
+// red must hold NTH * 32 floats and be free (the caller's last LDS use is complete
+// after the first barrier here).
+template <int NTH, int CPR>
 __device__ __forceinline__ void stats_flush(const GemmArgs& a, const float (&st)[2][2][8], int b0,
-                                            int m_last, int col0, int cpr, float* red) {
-    const int tid = threadIdx.x, nth = blockDim.x;
+                                            int m_last, int col0, float* red) {
+    const int tid = threadIdx.x;
     __syncthreads();
 #pragma unroll
     for (int sl = 0; sl < 2; ++sl)
@@ -86,14 +85,14 @@ __device__ __forceinline__ void stats_flush(const GemmArgs& a, const float (&st)
     __syncthreads();
     const int nslot = m_last / a.stats_hw != b0 ? 2 : 1;
     // value v of chunk c: slot v / 16, sum (0) or sum of squares (1) = (v / 8) % 2, column v % 8
-    for (int idx = tid; idx < cpr * 32; idx += nth) {
-        const int c = idx >> 5, v = idx & 31;
-        const int col = col0 + c * 8 + (v & 7);
-        if ((v >> 4) >= nslot || col >= a.N) continue;
-        float t = 0.f;
-        for (int r = c; r < nth; r += cpr) t += red[r * 32 + v];
-        atomicAdd(&a.stats[((int64_t)(b0 + (v >> 4)) * a.N + col) * 2 + ((v >> 3) & 1)], (double)t);
-    }
+    static_assert(CPR * 32 <= NTH, "one value per thread");
+    const int c = tid >> 5, v = tid & 31;
+    const int col = col0 + c * 8 + (v & 7);
+    if (tid >= CPR * 32 || (v >> 4) >= nslot || col >= a.N) return;
+    float t = 0.f;
+#pragma unroll
+    for (int j = 0; j < NTH / CPR; ++j) t += red[(c + j * CPR) * 32 + v];
+    atomicAdd(&a.stats[((int64_t)(b0 + (v >> 4)) * a.N + col) * 2 + ((v >> 3) & 1)], (double)t);
 }
 
 // Sum split-K partials and apply the epilogue.  Vector path: 8 output columns
@@ -809,7 +808,7 @@ void gemm_kernel(GemmArgs a) {
             }
         }
     }
-    if (do_st) stats_flush(a, st, st_b0, min(a.M, m0 + MT) - 1, n0, cpr, (float*)smem);
+    if (do_st) stats_flush<NTH, NT / 8>(a, st, st_b0, min(a.M, m0 + MT) - 1, n0, (float*)smem);
     if (do_rs) {
         // the cpr threads of a row are consecutive lanes, each 8 of them one 64-column
         // group: add their partial sums; the first of the 8 stores the group's partial

@@ -87,7 +87,7 @@ __global__ void geglu_kernel(const f16* g, f16* y, int T, int C2) {
     const int64_t t = i / C2;
     const int c = (int)(i - t * C2);
     const float a = (float)g[t * 2 * C2 + c], bb = (float)g[t * 2 * C2 + C2 + c];
-    y[i] = (f16)(a * (0.5f * bb * (1.0f + erff(bb * 0.70710678118654752f))));
+    y[i] = (f16)(a * gelu_erf(bb));
 }
 
 hipError_t silu_launch(const f16* x, f16* y, int64_t n, hipStream_t s) {

@@ -12,6 +12,17 @@ namespace sdu {
 
 typedef _Float16 f16;
 
+// GELU with the erf of Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7): the branch-free
+// form the reference's geglu_f32.comp evaluates, gelu(x) = 0.5 x (1 + erf(x / sqrt 2)).
+__device__ __forceinline__ float erf_as(float x) {
+    const float ax = fabsf(x);
+    const float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * ax);
+    const float p = ((((1.061405429f * t - 1.453152027f) * t + 1.421413741f) * t - 0.284496736f) * t +
+                     0.254829592f) * t;
+    return copysignf(1.0f - p * __expf(-ax * ax), x);
+}
+__device__ __forceinline__ float gelu_erf(float x) { return 0.5f * x * (1.0f + erf_as(x * 0.70710678118654752f)); }
+
 // ----------------------------------------------------------------- kernel timing
 // Eager profiling hook.  While a KernelTimer is installed on the calling thread
 // (only inside sdu_profile, never during graph capture), every kernel launch of
