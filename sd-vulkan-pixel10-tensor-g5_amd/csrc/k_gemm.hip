@@ -830,6 +830,86 @@ void gemm_kernel(GemmArgs a) {
     }
 }
 
+// 3x3 conv (pad 1, stride 1, no upsample) with at most 8 output channels (the UNet's
+// conv_out, 320 -> 4): an MFMA tile would be 64 columns wide for 4, and 64 such tiles
+// cannot fill the chip.  One thread per (pixel, K slice), 16 pixels x 16 slices per
+// block: slice s takes the 8-channel chunks j = s, s + 16, ... of the pixel's 9 Cin / 8
+// (tap-major, as W's K index) with fp16 dot products into fp32, the weights staged
+// in LDS (dynamic, CO * 9 * Cin * 2 bytes); the 16 slices of a pixel are consecutive
+// lanes, added by shuffles, and the first runs the common epilogue.  Loads go in
+// batches of 12 chunks (two batches at Cin = 320), all issued before any is used.
+constexpr int kNarrowPix = 16, kNarrowSlices = 16, kNarrowBatch = 12;
+template <int CO>
+__global__ __launch_bounds__(256) void conv3_narrow_kernel(GemmArgs a) {
+    typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+    extern __shared__ uint4 wsm[];  // [CO][nchunk]
+    const int cpt = a.Cin / 8, nchunk = 9 * cpt;
+    {
+        // CO * nchunk <= 4096 chunks (narrow_conv): at most 16 per thread, loads first
+        constexpr int SMAX = 4096 / (kNarrowPix * kNarrowSlices);
+        uint4 wv[SMAX];
+#pragma unroll
+        for (int u = 0; u < SMAX; ++u) {
+            const int i = threadIdx.x + u * kNarrowPix * kNarrowSlices, co = i / nchunk, j = i - co * nchunk;
+            wv[u] = make_uint4(0, 0, 0, 0);
+            if (i < CO * nchunk && co < a.N) wv[u] = *(const uint4*)(a.Wt + (int64_t)co * a.K + j * 8);
+        }
+#pragma unroll
+        for (int u = 0; u < SMAX; ++u) {
+            const int i = threadIdx.x + u * kNarrowPix * kNarrowSlices;
+            if (i < CO * nchunk) wsm[i] = wv[u];
+        }
+    }
+    __syncthreads();
+    const int tid = threadIdx.x, sl = tid % kNarrowSlices;
+    const int p = blockIdx.x * kNarrowPix + tid / kNarrowSlices;
+    const int m = min(p, a.M - 1);
+    const int hw = a.Ho * a.Wo, bb = m / hw, r = m - bb * hw, oy = r / a.Wo, ox = r - oy * a.Wo;
+    float acc[CO];
+#pragma unroll
+    for (int co = 0; co < CO; ++co) acc[co] = 0.f;
+    // chunks in batches: every load of a batch issued before any is used
+    for (int j0 = sl; j0 < nchunk; j0 += kNarrowSlices * kNarrowBatch) {
+        uint4 x[kNarrowBatch];
+#pragma unroll
+        for (int u = 0; u < kNarrowBatch; ++u) {
+            const int j = j0 + u * kNarrowSlices;
+            const int tap = j / cpt, c8 = j - tap * cpt;
+            const int iy = oy + tap / 3 - 1, ix = ox + tap % 3 - 1;
+            x[u] = make_uint4(0, 0, 0, 0);
+            if (j < nchunk && iy >= 0 && iy < a.Hin && ix >= 0 && ix < a.Win)
+                x[u] = *(const uint4*)(a.A + (((int64_t)bb * a.Hin + iy) * a.Win + ix) * a.Cin + c8 * 8);
+        }
+#pragma unroll
+        for (int u = 0; u < kNarrowBatch; ++u) {
+            const int j = j0 + u * kNarrowSlices;
+            if (j >= nchunk) break;
+            const half2v* xh = (const half2v*)&x[u];
+#pragma unroll
+            for (int co = 0; co < CO; ++co) {
+                const uint4 w = wsm[co * nchunk + j];
+                const half2v* wh = (const half2v*)&w;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) acc[co] = __builtin_amdgcn_fdot2(xh[q], wh[q], acc[co], false);
+            }
+        }
+    }
+#pragma unroll
+    for (int co = 0; co < CO; ++co)
+#pragma unroll
+        for (int off = 1; off < kNarrowSlices; off <<= 1) acc[co] += __shfl_xor(acc[co], off);
+    if (sl != 0 || p >= a.M) return;
+#pragma unroll
+    for (int co = 0; co < CO; ++co)
+        if (co < a.N) epi_store(a, p, co, acc[co], 0.f, co);
+}
+
+// The narrow conv takes a 3x3 conv when its weights (up to 8 outputs) fit 64 KB of LDS.
+bool narrow_conv(const GemmArgs& a) {
+    return a.amode == A_CONV3 && a.N <= 8 && a.stride == 1 && !a.upsample && !a.A2 && !a.stats && !a.geglu &&
+           !a.row_part && a.Cin % 8 == 0 && 8 * 9 * (a.Cin / 8) <= 4096 && a.M > 0;
+}
+
 namespace {
 struct Cfg {
     int mt, nt, per_cu;   // tile, resident blocks per CU (LDS-limited)
@@ -916,6 +996,7 @@ void plan(const GemmArgs& a, int& ci, int& splits, int& kps, bool& fix) {
 bool gemm_stats_supported(int hw) { return stats_tile_ok(128, hw); }
 
 const char* gemm_kernel_name(const GemmArgs& a) {
+    if (narrow_conv(a)) return a.N <= 4 ? "conv3_narrow_kernel<4>" : "conv3_narrow_kernel<8>";
     int ci, splits, kps;
     bool fix;
     plan(a, ci, splits, kps, fix);
@@ -925,6 +1006,7 @@ const char* gemm_kernel_name(const GemmArgs& a) {
 size_t gemm_counter_bytes() { return kCounterBytes; }
 
 size_t gemm_workspace_bytes(const GemmArgs& a) {
+    if (narrow_conv(a)) return 0;
     int ci, splits, kps;
     bool fix;
     plan(a, ci, splits, kps, fix);
@@ -942,6 +1024,24 @@ static void launch_cfg(int ci, dim3 grid, const GemmArgs& a, hipStream_t s) {
 }
 
 hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s) {
+    if (narrow_conv(a)) {
+        if (a.Ho != a.Hin || a.Wo != a.Win || a.M != a.Bn * a.Ho * a.Wo || a.K != 9 * a.Cin ||
+            2 * (int64_t)a.Bn * a.Hin * a.Win * a.Cin > 0x7fffffff)
+            return hipErrorInvalidValue;
+        a.splits = 1;
+        a.partial = nullptr;
+        const int co = a.N <= 4 ? 4 : 8;
+        const size_t lds = (size_t)co * 9 * a.Cin * 2;
+        const dim3 grid((a.M + kNarrowPix - 1) / kNarrowPix);
+        const double flops = 2.0 * a.M * a.N * a.K;
+        const double bytes = 2.0 * a.Bn * a.Hin * a.Win * a.Cin + 2.0 * a.N * a.K +
+                             (double)a.M * a.N * (a.out_mode == OUT_F16 ? 2.0 : 4.0) + (a.res ? 2.0 * a.M * a.N : 0.0);
+        launch_timed(co == 4 ? "conv3_narrow_kernel<4>" : "conv3_narrow_kernel<8>", flops, bytes, [&] {
+            if (co == 4) hipLaunchKernelGGL(conv3_narrow_kernel<4>, grid, dim3(kNarrowPix * kNarrowSlices), lds, s, a);
+            else hipLaunchKernelGGL(conv3_narrow_kernel<8>, grid, dim3(kNarrowPix * kNarrowSlices), lds, s, a);
+        });
+        return hipGetLastError();
+    }
     int ci, splits, kps;
     bool fix;
     plan(a, ci, splits, kps, fix);
