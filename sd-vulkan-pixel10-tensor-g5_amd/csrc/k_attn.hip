@@ -253,7 +253,11 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_kernel(AttnArgs a) {
     for (int it = 0; it < nt; ++it) {
         const int buf = it & 1;
         const int kb = it * KT;
+        // wave priority: highest while issuing the next tile's loads, raised through
+        // the scores, softmax and PV, normal for the LDS stores and the barrier
+        __builtin_amdgcn_s_setprio(2);
         if (it + 1 < nt) load_kv(kb + KT);
+        __builtin_amdgcn_s_setprio(1);
 
         floatx16 s[2];
 #pragma unroll
@@ -267,6 +271,7 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_kernel(AttnArgs a) {
             }
         }
         softmax_pv<2, MTD, LSUM>(s, min(KT, a.Sk - kb), c, m_run, l_run, o, Vt[buf], VSTR, hl, lrow, lk);
+        __builtin_amdgcn_s_setprio(0);
         if (it + 1 < nt) store_kv(buf ^ 1);
         __syncthreads();
     }
@@ -405,8 +410,12 @@ __global__ __launch_bounds__(NSPLIT * 64) void attn_split_kernel(AttnArgs a) {
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
             s[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[ks], qf[ks], s[0], 0, 0, 0);
+        // wave priority as in attn_kernel: the next tile's loads first, then the softmax / PV
+        __builtin_amdgcn_s_setprio(2);
         if (it + NSPLIT < ntile) load(kb + NSPLIT * KTS);
+        __builtin_amdgcn_s_setprio(1);
         softmax_pv<1, MTD, LSUM>(s, min(KTS, a.Sk - kb), c, m_run, l_run, o, vt, VSTRS, hl, lrow, lk);
+        __builtin_amdgcn_s_setprio(0);
         __builtin_amdgcn_wave_barrier();
     }
 
