@@ -263,18 +263,23 @@ __global__ void zero_kernel(uint4* p, int64_t n16) {
 
 static constexpr int GNF_THREADS = 1024;
 
-// Sum over the block of one float per thread, in fp64 across waves; every thread
-// gets the result.
-__device__ __forceinline__ double gnf_block_sum(float v, double* red) {
+// Sums over the block of two floats per thread, in fp64 across waves; every thread
+// gets the results.
+__device__ __forceinline__ double2 gnf_block_sum2(float v, float u, double2* red) {
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    for (int off = 32; off > 0; off >>= 1) {
+        v += __shfl_xor(v, off);
+        u += __shfl_xor(u, off);
+    }
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    __syncthreads();  // red[] may still be read by the previous reduction
-    if (lane == 0) red[wave] = (double)v;
+    if (lane == 0) red[wave] = make_double2((double)v, (double)u);
     __syncthreads();
-    double t = 0.0;
+    double2 t = make_double2(0.0, 0.0);
 #pragma unroll
-    for (int w = 0; w < GNF_THREADS / 64; ++w) t += red[w];
+    for (int w = 0; w < GNF_THREADS / 64; ++w) {
+        t.x += red[w].x;
+        t.y += red[w].y;
+    }
     return t;
 }
 
@@ -309,7 +314,7 @@ __global__ __launch_bounds__(GNF_THREADS) void gn_fused_kernel(const f16* x, con
                                                                const f16* gamma, const f16* beta, f16* y,
                                                                int B, int HW, int G, float eps, int silu) {
     typedef typename GnfVec<VW>::T V;
-    __shared__ double red[GNF_THREADS / 64];
+    __shared__ double2 red[GNF_THREADS / 64];
     const int C = C1 + C2, cpg = C / G, vpg = cpg / VW;
     const int g = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
     const int P = GNF_THREADS / vpg;
@@ -329,31 +334,30 @@ __global__ __launch_bounds__(GNF_THREADS) void gn_fused_kernel(const f16* x, con
 #pragma unroll
         for (int k = 0; k < EP; ++k) raw[k] = GnfVec<VW>::load(rs, vo + min(pp + k * P, HW - 1) * Cs * 2);
     }
-    float s = 0.f;
-#pragma unroll
-    for (int k = 0; k < EP; ++k) {
-        if (act && pp + k * P < HW) {
-            const f16* h = (const f16*)&raw[k];
-#pragma unroll
-            for (int e = 0; e < VW; ++e) s += (float)h[e];
-        }
-    }
-    const double n = (double)HW * cpg;
-    const double mean = gnf_block_sum(s, red) / n;
-    const float mf = (float)mean;
-    float ss = 0.f;
+    // One pass over the values shifted by the group's first value (the same element
+    // for every thread): the sum and sum of squares of x - shift do not cancel for a
+    // group whose mean is large against its spread.  (x - shift is exact in fp32.)
+    const int c0 = g * cpg;
+    const float shift = (float)(c0 < C1 ? x[(int64_t)b * HW * C1 + c0] : x2[(int64_t)b * HW * C2 + (c0 - C1)]);
+    float s = 0.f, ss = 0.f;
 #pragma unroll
     for (int k = 0; k < EP; ++k) {
         if (act && pp + k * P < HW) {
             const f16* h = (const f16*)&raw[k];
 #pragma unroll
             for (int e = 0; e < VW; ++e) {
-                const float dv = (float)h[e] - mf;
+                const float dv = (float)h[e] - shift;
+                s += dv;
                 ss += dv * dv;
             }
         }
     }
-    const double var = gnf_block_sum(ss, red) / n;
+    const double n = (double)HW * cpg;
+    const double2 t = gnf_block_sum2(s, ss, red);
+    const double m1 = t.x / n;
+    const double mean = shift + m1;
+    const double var = fmax(t.y / n - m1 * m1, 0.0);
+    const float mf = (float)mean;
     const float rstd = (float)(1.0 / sqrt(var + (double)eps));
     float sc[VW], sh[VW];
 #pragma unroll

@@ -62,6 +62,29 @@ def test_groupnorm(op_engine, B, H, W, C1, C2, silu):
     assert np.array_equal(ty.numpy().astype(np.float32), got)
 
 
+@pytest.mark.parametrize("B,H,W,C,silu", [(2, 32, 32, 640, True), (2, 16, 16, 1280, False)])
+def test_groupnorm_large_mean(op_engine, B, H, W, C, silu):
+    """Groups whose mean is 100x their spread (the single-kernel path sums x minus the
+    group's first value in one pass; without the shift an fp32 one-pass variance of
+    these values cancels to noise)."""
+    say(f"groupnorm large mean B={B} {H}x{W} C={C}")
+    HW = H * W
+    x = r16((B, HW, C), 11, 1.0, 100.0)
+    g = r16((C,), 2, 0.3, 1.0)
+    b = r16((C,), 3, 0.3)
+    e = op_engine
+    tx = e.upload(x.astype(np.float16))
+    tg, tb = e.upload(g.astype(np.float16)), e.upload(b.astype(np.float16))
+    ty = e.tensor((B, HW, C))
+    e.groupnorm(tx, tg, tb, ty, B, HW, C, 0, silu=silu)
+    got = ty.numpy().astype(np.float32)
+    xn = t(x.transpose(0, 2, 1).reshape(B, C, H, W)).double()
+    ref = U.group_norm(xn, t(g).double(), t(b).double(), act_silu=silu).float().numpy()
+    ref = ref.reshape(B, C, HW).transpose(0, 2, 1)
+    assert rel_err_l1(got, ref) < 1e-3
+    assert np.abs(got - ref).max() < 2e-2
+
+
 # ------------------------------------------------------------------ LayerNorm
 
 
