@@ -131,12 +131,17 @@ int sdu_set_weight(sdu_ctx* ctx, const char* name, const float* data, int64_t nu
         };
         static const char* const kFoldSources[] = {
             ".ff.net.2.weight", ".ff.net.2.bias", ".proj_out.weight", ".proj_out.bias",    // FF out + proj_out
-            ".conv2.weight", ".conv2.bias", ".conv_shortcut.weight", ".conv_shortcut.bias",  // resnet shortcut
-            ".norm1.weight", ".norm1.bias", ".attn1.to_q.weight", ".attn1.to_k.weight",     // LayerNorm folds
-            ".attn1.to_v.weight", ".norm2.weight", ".norm2.bias", ".attn2.to_q.weight",
-            ".norm3.weight", ".norm3.bias", ".ff.net.0.proj.weight", ".ff.net.0.proj.bias"};
+            ".conv2.weight", ".conv2.bias", ".conv_shortcut.weight", ".conv_shortcut.bias"};  // resnet shortcut
+        // LayerNorm folds (a resnet's norm1 / norm2 are GroupNorms, not folded)
+        static const char* const kLnFoldSources[] = {
+            ".norm1.weight", ".norm1.bias", ".attn1.to_q.weight", ".attn1.to_k.weight", ".attn1.to_v.weight",
+            ".norm2.weight", ".norm2.bias", ".attn2.to_q.weight", ".norm3.weight", ".norm3.bias",
+            ".ff.net.0.proj.weight", ".ff.net.0.proj.bias"};
         for (const char* suf : kFoldSources)
             if (ends(suf)) return fold_weights(ctx->c, n);
+        if (n.find(".transformer_blocks.") != std::string::npos)
+            for (const char* suf : kLnFoldSources)
+                if (ends(suf)) return fold_weights(ctx->c, n);
         return SDU_OK;
     });
 }

@@ -910,7 +910,7 @@ __global__ __launch_bounds__(256) void conv3_narrow_kernel(GemmArgs a) {
 }
 
 // The narrow conv takes a 3x3 conv when its weights (up to 8 outputs) fit 64 KB of LDS.
-bool narrow_conv(const GemmArgs& a) {
+static bool narrow_conv(const GemmArgs& a) {
     return a.amode == A_CONV3 && a.N <= 8 && a.stride == 1 && !a.upsample && !a.A2 && !a.stats && !a.geglu &&
            !a.row_part && a.Cin % 8 == 0 && 8 * 9 * (a.Cin / 8) <= 4096 && a.M > 0;
 }
