@@ -226,6 +226,12 @@ __global__ void splitk_reduce_kernel(GemmArgs a) {
     else reduce_rows<1, false>(a, m, 1u, nout, o);
 }
 
+// 8 consecutive fp32 values from 16-byte-aligned LDS
+__device__ __forceinline__ void ld8(const float* p, float (&v)[8]) {
+    const float4 x = *(const float4*)p, y = *(const float4*)(p + 4);
+    v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w; v[4] = y.x; v[5] = y.y; v[6] = y.z; v[7] = y.w;
+}
+
 // Main loop: NS-stage LDS ring fed by global_load_lds_dwordx4 (direct to LDS, no
 // register staging), NS-1 K tiles in flight while one is consumed, one s_barrier
 // per K tile.  LDS rows are BK halves (64 or 128 bytes) with the 16-byte chunk
@@ -233,12 +239,6 @@ __global__ void splitk_reduce_kernel(GemmArgs a) {
 // 32x32x16 fragment reads (32 rows x 16 B per half-wave) are free of bank
 // conflicts.  Fragments are double-buffered in registers: the LDS reads of
 // k-step ks+1 are in flight during the MFMAs of k-step ks.
-// 8 consecutive fp32 values from 16-byte-aligned LDS
-__device__ __forceinline__ void ld8(const float* p, float (&v)[8]) {
-    const float4 x = *(const float4*)p, y = *(const float4*)(p + 4);
-    v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w; v[4] = y.x; v[5] = y.y; v[6] = y.z; v[7] = y.w;
-}
-
 template <int BKT>
 __device__ __forceinline__ int lds_swizzle(int row) {
     return BKT == 64 ? ((row >> 1) & 7) : ((row >> 2) & 3);
