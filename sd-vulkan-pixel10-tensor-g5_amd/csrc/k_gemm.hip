@@ -945,7 +945,7 @@ int fix_slots_per_round(int mt, int nt) {
     const int f = (mt / 64) * (nt / 64);  // 32x32 fragments per wave (8 waves)
     return f >= 4 ? 1 : 4 / f;
 }
-constexpr double kFixBase = 1.0e-6, kFixRound = 1.2e-6;
+constexpr double kFixBase = 1.0e-6, kFixRound = 0.9e-6;
 
 // The epilogue keeps output statistics for two images per tile: the MT rows of a tile
 // (MT-aligned) must not reach a third image.
