@@ -27,29 +27,72 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 METRIC = "UNet forwards/sec (B=2, 64x64, fp16) on 1 MI355X; ms per 4-step LCM denoise"
 
 
-def cpu_baseline(B=2, H=64, W=64, timed=2):
-    """The oracle's fp32 torch forward on the host cores (B=2 64x64 sample)."""
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(H=64, W=64, timed=3):
+    """The oracle's fp32 torch forward on the host cores: B=2 (the headline workload,
+    `value`) and B=1 (the single-image CPU reference forward), each 1 warm-up then the
+    median of `timed` forwards (the method of tools/bench_cpu.py:34-41)."""
     import numpy as np
     import torch
     from oracle import lcm, unet_ref, weights
     threads = min(os.cpu_count() or 1, 64)
     torch.set_num_threads(threads)
     p = unet_ref.to_torch(weights.generate(1234))
-    lat = weights.gauss("input.latent", (B, 4, H, W), 1, fp16=False)
-    ctx = weights.gauss("input.context", (B, 77, 768), 1, fp16=False)
     temb = lcm.time_proj(999)
-    ts = []
-    with torch.inference_mode():
-        unet_ref.unet_forward(p, lat, temb, ctx)  # warm-up
-        for _ in range(timed):
-            t0 = time.perf_counter()
-            unet_ref.unet_forward(p, lat, temb, ctx)
-            ts.append(time.perf_counter() - t0)
-    med = float(np.median(ts))
-    return {"value": 1.0 / med, "unit": f"UNet forwards/sec (B={B}, {H}x{W}, fp32, CPU)",
-            "cores": threads, "kind": "port",
-            "sample": f"1 warm-up + median of {timed} B={B} {H}x{W} fp32 forwards of the oracle "
-                      f"({med:.2f} s each)"}
+    res = {}
+    for B in (2, 1):
+        lat = weights.gauss("input.latent", (B, 4, H, W), 1, fp16=False)
+        ctx = weights.gauss("input.context", (B, 77, 768), 1, fp16=False)
+        ts = []
+        with torch.inference_mode():
+            unet_ref.unet_forward(p, lat, temb, ctx)  # warm-up
+            for _ in range(timed):
+                t0 = time.perf_counter()
+                unet_ref.unet_forward(p, lat, temb, ctx)
+                ts.append(time.perf_counter() - t0)
+        res[B] = (float(np.median(ts)), [round(x, 3) for x in ts])
+    med2, med1 = res[2][0], res[1][0]
+    return {"value": round(1.0 / med2, 4), "unit": f"UNet forwards/sec (B=2, {H}x{W}, fp32, CPU)",
+            "cores": threads, "kind": "port", "cpu_model": cpu_model(),
+            "sample": f"oracle fp32 forwards at {H}x{W}: 1 warm-up + median of {timed} timed, "
+                      f"B=2 {med2:.2f} s (runs {res[2][1]}), B=1 {med1:.2f} s (runs {res[1][1]})",
+            "b1_forwards_per_s": round(1.0 / med1, 4), "b1_s_per_forward": round(med1, 3),
+            "b2_s_per_forward": round(med2, 3)}
+
+
+# per-op roofline ideal per forward (sum over ops of max(FLOP / 2.5 PF, bytes / 8 TB/s),
+# fp16 operands moved once per op): B=2 64x64, B=2 96x96, B=16 64x64
+ROOFLINE_IDEAL_MS = {(2, 64): 0.907, (2, 96): 2.18, (16, 64): 6.71}
+
+
+def time_forward(eng, sdu, rng, B, H, W, L, steps, warmup):
+    import numpy as np
+    lat = rng.standard_normal((B, 4, H, W), np.float32)
+    ctx = rng.standard_normal((B, L, 768), np.float32)
+    d_lat, d_ctx, d_temb = eng.upload(lat), eng.upload(ctx), eng.upload(sdu.time_proj(999))
+    d_out = eng.tensor((B, 4, H, W), sdu.SDU_F32)
+
+    def fwd():
+        eng.forward_device(d_lat.ptr, d_temb.ptr, d_ctx.ptr, B, H, W, L, d_out.ptr)
+    for _ in range(warmup):
+        fwd()
+    eng.sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fwd()
+    eng.sync()
+    dt = time.perf_counter() - t0
+    return dt / steps * 1e3, d_out
 
 
 def measured_traffic(kernel):
@@ -97,13 +140,13 @@ def main():
     import numpy as np
     import torch
     import sdu
-    from oracle import lcm, weights  # input generation only (same seeded stream as the tests)
 
     B, H, W, L = 2, 64, 64, 77
     eng = sdu.Engine(seed=1234)
-    lat = weights.gauss("input.latent", (B, 4, H, W), 1, fp16=False)
-    ctx = weights.gauss("input.context", (B, L, 768), 1, fp16=False)
-    temb = lcm.time_proj(999)
+    rng = np.random.default_rng(1)
+    lat = rng.standard_normal((B, 4, H, W), np.float32)
+    ctx = rng.standard_normal((B, L, 768), np.float32)
+    temb = sdu.time_proj(999)
     d_lat, d_ctx, d_temb = eng.upload(lat), eng.upload(ctx), eng.upload(temb)
     d_out = eng.tensor((B, 4, H, W), sdu.SDU_F32)
 
@@ -137,10 +180,10 @@ def main():
 
     # 4-step LCM + CFG denoise (guidance 8), device-resident
     steps = 4
-    lat1 = weights.gauss("input.latent", (4, H, W), 2, fp16=False)
-    cond = weights.gauss("input.cond", (L, 768), 2, fp16=False)
-    unc = weights.gauss("input.uncond", (L, 768), 2, fp16=False)
-    noise = weights.gauss("input.noise", (steps - 1, 4, H, W), 2, fp16=False)
+    lat1 = rng.standard_normal((4, H, W), np.float32)
+    cond = rng.standard_normal((L, 768), np.float32)
+    unc = rng.standard_normal((L, 768), np.float32)
+    noise = rng.standard_normal((steps - 1, 4, H, W), np.float32)
     dl, dc, du, dn = eng.upload(lat1), eng.upload(cond), eng.upload(unc), eng.upload(noise)
     dlo = eng.tensor((4, H, W), sdu.SDU_F32)
 
@@ -156,8 +199,8 @@ def main():
     eng.sync()
     lcm_ms = (time.perf_counter() - t0) / args.lcm_reps * 1e3
 
-    # per-kernel profile: every kernel timed on its own with HIP events on the engine
-    # stream (each launch repeated back to back between its events, average kept)
+    # per-kernel profile: every kernel launch of one eager forward timed on its own with
+    # HIP events on the engine stream
     prof, prof_total = eng.profile(B, H, W, L)
     kernels = {k[2:]: v for k, v in prof.items() if k.startswith("k:")}
     cats = {k: v for k, v in prof.items() if not k.startswith("k:")}
@@ -173,6 +216,8 @@ def main():
                 "frac": round(ach / PEAK_HBM_GBS, 4)}
     traffic = measured_traffic(dom_name)
     roof.update({"traffic": traffic, "kernel": dom_name, "calls": dom["calls"],
+                 "timing": "HIP events around each launch (one launch each) on the engine stream, "
+                           "eager profiling forward",
                  "flops_per_launch": dom["flops"] / dom["calls"],
                  "bytes_per_launch": dom["bytes"] / dom["calls"],
                  "avg_launch_us": round(avg_us, 3)})
@@ -188,6 +233,15 @@ def main():
         per_kernel[k] = e
     per_cat = {k: {"calls": v["calls"], "ms": round(v["ms"], 4)} for k, v in
                sorted(cats.items(), key=lambda kv: -kv[1]["ms"])}
+
+    # the other single-GPU shapes: B=2 96x96 (9216-token attention) and B=16 64x64
+    extra = {}
+    for (b, hw, n) in ((2, 96, max(5, args.steps // 4)), (16, 64, max(5, args.steps // 8))):
+        ms, _ = time_forward(eng, sdu, rng, b, hw, hw, L, n, 3)
+        ideal = ROOFLINE_IDEAL_MS[(b, hw)]
+        extra[f"b{b}_{hw}x{hw}"] = {"ms_per_forward": round(ms, 3), "forwards_per_s": round(1e3 / ms, 2),
+                                    "images_per_s": round(b * 1e3 / ms, 1), "steps": n,
+                                    "roofline_ideal_ms": ideal, "frac_of_roofline": round(ideal / ms, 4)}
 
     cpu = None if args.no_cpu else cpu_baseline()
     eng.release()
@@ -207,7 +261,9 @@ def main():
         "data": "synthetic (seeded N(0,1) latent/context, seeded random-init weights)",
         "config": {"workload": "SD1.5 UNet forward, batch-CFG B=2, 2x4x64x64 latent, 2x77x768 context",
                    "global_batch": B, "latent": [H, W], "context_tokens": L, "parallelism": "single GPU"},
+        "frac_of_roofline": round(ROOFLINE_IDEAL_MS[(2, 64)] / ms_step, 4),
         "lcm_4step_ms": round(lcm_ms, 3),
+        "other_shapes": extra,
         "host_io_forwards_per_s": round(host_fps, 3),
         "roofline": roof,
         "cpu_baseline": cpu,

@@ -93,6 +93,11 @@ int sdu_denoise_lcm(sdu_ctx* ctx, const float* lat, const float* cond, const flo
                     int H, int W, int L, int steps, float guidance, const float* noise,
                     float* out);
 
+/* timeProj (VulkanUnetPipeline.kt:36-46): the 320-d timestep embedding the forward
+ * takes as temb, out = [cos(t f_i) (160) | sin(t f_i) (160)], f_i = exp(-ln(1e4) i/160),
+ * evaluated in float64 and rounded to float32.  0 <= t <= 100000; needs no context. */
+int sdu_time_proj(int t, float* out);
+
 /* Device-resident variants for throughput runs: every pointer is device memory
  * (same layouts and dtypes as above).  Enqueued on the context stream; the first
  * call for a shape records a HIP graph, later calls replay it. */
@@ -112,7 +117,12 @@ int sdu_denoise_lcm_device(sdu_ctx* ctx, const float* d_lat, const float* d_cond
  *    element i = float(sqrt(-2 ln u1) cos(2 pi u2)) of the seeded generator with
  *    key = fnv1a64("lcm.noise") ^ splitmix64(noise_seed) (:100 draws it from its own
  *    RNG; the stream differs, the distribution is the same).
- * Each (H, W, L, steps, guidance, cfg_steps) records its own HIP graph. */
+ * Each (H, W, L, steps, CFG pattern) records its own HIP graph, where the CFG pattern
+ * is the number of batch-CFG steps (0 when guidance <= 1); the guidance value is read
+ * by the graph from device memory written before each replay, so any number of
+ * guidance values share one graph.  A non-finite guidance is SDU_ERR_ARG.  A context
+ * keeps at most 16 planned shapes (forward and denoise) and evicts the least recently
+ * used one to plan another. */
 int sdu_denoise_lcm_ex(sdu_ctx* ctx, const float* d_lat, const float* d_cond,
                        const float* d_uncond, int H, int W, int L, int steps, float guidance,
                        int cfg_steps, const float* d_noise, uint64_t noise_seed, float* d_out);
@@ -123,12 +133,26 @@ int sdu_denoise_lcm_ex(sdu_ctx* ctx, const float* d_lat, const float* d_cond,
  * relErr_L1 = sum|ref-got| / sum|ref| over the three outputs; negative on error. */
 double sdu_selftest(sdu_ctx* ctx, const char* fixture_dir);
 
+/* The legs of unetSelfTest (vk_engine.cpp:811-851) one by one:
+ *  - relerr_b1: the B=1 forward vs OUT_y (:818-821);
+ *  - relerr_b2[2]: both images of the B=2 run with the input in both slots (:823-839);
+ *  - ctx_sens: when fixture_dir holds IN_cond.bin, IN_unc.bin (fp16 [77,768]) and
+ *    IN_temb999.bin (fp16 [320]), the mean |eps_cond - eps_unc| of two B=1 forwards of
+ *    IN_lat under those contexts (:840-849; the reference logs it next to its PyTorch
+ *    value), else -1. */
+typedef struct sdu_selftest_report {
+    double relerr_b1;
+    double relerr_b2[2];
+    double ctx_sens;
+} sdu_selftest_report;
+int sdu_selftest_ex(sdu_ctx* ctx, const char* fixture_dir, sdu_selftest_report* out);
+
 /* unetProfile (vk_engine.cpp:854-872): one eager forward in which every kernel
- * launch is timed on its own with HIP events on the context stream (the launch is
- * repeated SDU_PROFILE_REPS times, default 5, between its events and the average
- * kept).  Entries are accumulated per op category (e.g. "conv3x3") and per kernel
- * ("k:" + kernel name, e.g. "k:gemm_kernel<128,128,2,2,64,2>"); total_ms sums the
- * categories.  The activations of the profiled pass are not meaningful. */
+ * launch is timed on its own with HIP events on the context stream (each launch once
+ * between its events; the environment variable SDU_PROFILE_REPS > 1 repeats it and
+ * keeps the average, at the cost of meaningless activations in that pass).  Entries
+ * are accumulated per op category (e.g. "conv3x3") and per kernel ("k:" + kernel
+ * name, e.g. "k:gemm_kernel<128,128,2,2,64,2>"); total_ms sums the categories. */
 typedef struct sdu_prof_entry {
     char name[48];
     int calls;

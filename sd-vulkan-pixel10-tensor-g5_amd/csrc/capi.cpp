@@ -251,14 +251,16 @@ int sdu_denoise_lcm(sdu_ctx* ctx, const float* lat, const float* cond, const flo
     });
 }
 
-double sdu_selftest(sdu_ctx* ctx, const char* fixture_dir) {
-    if (!ctx) return (double)SDU_ERR_NOT_INIT;
-    if (!fixture_dir) return (double)fail(ctx, SDU_ERR_ARG, "null fixture dir");
-    try {
-        // unetSelfTest protocol (vk_engine.cpp:811-839): fp16 IN_lat / IN_ctx /
-        // IN_temb_proj, B=1 forward vs OUT_y, then B=2 with the input in both slots.
+int sdu_selftest_ex(sdu_ctx* ctx, const char* fixture_dir, sdu_selftest_report* out) {
+    SDU_GUARD(ctx);
+    if (!fixture_dir || !out) return fail(ctx, SDU_ERR_ARG, "null argument");
+    return guarded(ctx, [&]() -> int {
+        // unetSelfTest protocol (vk_engine.cpp:811-851): fp16 IN_lat / IN_ctx /
+        // IN_temb_proj, B=1 forward vs OUT_y, then B=2 with the input in both slots,
+        // then (if present) the context-sensitivity pair IN_cond / IN_unc at IN_temb999.
+        auto path = [&](const char* nm) { return std::string(fixture_dir) + "/" + nm + ".bin"; };
         auto load = [&](const char* nm, size_t n, std::vector<float>& v) -> bool {
-            std::ifstream f(std::string(fixture_dir) + "/" + nm + ".bin", std::ios::binary);
+            std::ifstream f(path(nm), std::ios::binary);
             if (!f) return false;
             std::vector<f16> h(n);
             if (!f.read((char*)h.data(), n * 2)) return false;
@@ -270,7 +272,8 @@ double sdu_selftest(sdu_ctx* ctx, const char* fixture_dir) {
         std::vector<float> lat, cx, tp, ref;
         if (!load("IN_lat", LAT, lat) || !load("IN_ctx", CTX, cx) || !load("IN_temb_proj", 320, tp) ||
             !load("OUT_y", LAT, ref))
-            return (double)fail(ctx, SDU_ERR_IO, "self-test fixture missing");
+            return fail(ctx, SDU_ERR_IO, "self-test fixture missing");
+        // corrCheck (vk_engine.cpp:698-704) over every element
         auto rel = [&](const float* got) {
             double se = 0, sr = 0;
             for (size_t i = 0; i < LAT; ++i) { se += std::fabs(ref[i] - got[i]); sr += std::fabs(ref[i]); }
@@ -278,19 +281,46 @@ double sdu_selftest(sdu_ctx* ctx, const char* fixture_dir) {
         };
         std::vector<float> y1(LAT), y2(2 * LAT);
         int st = unet_forward_host(ctx->c, lat.data(), tp.data(), cx.data(), 1, 64, 64, 77, y1.data());
-        if (st) return (double)st;
+        if (st) return st;
         std::vector<float> lat2(2 * LAT), cx2(2 * CTX);
         memcpy(lat2.data(), lat.data(), LAT * 4);
         memcpy(lat2.data() + LAT, lat.data(), LAT * 4);
         memcpy(cx2.data(), cx.data(), CTX * 4);
         memcpy(cx2.data() + CTX, cx.data(), CTX * 4);
         st = unet_forward_host(ctx->c, lat2.data(), tp.data(), cx2.data(), 2, 64, 64, 77, y2.data());
-        if (st) return (double)st;
-        const double e0 = rel(y1.data()), e1 = rel(y2.data()), e2 = rel(y2.data() + LAT);
-        return std::max(e0, std::max(e1, e2));
-    } catch (...) {
-        return (double)fail(ctx, SDU_ERR_OOM, "self-test failed");
-    }
+        if (st) return st;
+        out->relerr_b1 = rel(y1.data());
+        out->relerr_b2[0] = rel(y2.data());
+        out->relerr_b2[1] = rel(y2.data() + LAT);
+        out->ctx_sens = -1.0;
+        std::vector<float> cc, uc, t999;
+        if (std::ifstream(path("IN_cond")).good()) {
+            if (!load("IN_cond", CTX, cc) || !load("IN_unc", CTX, uc) || !load("IN_temb999", 320, t999))
+                return fail(ctx, SDU_ERR_IO, "context-sensitivity fixture missing or short");
+            std::vector<float> ec(LAT), eu(LAT);
+            if ((st = unet_forward_host(ctx->c, lat.data(), t999.data(), cc.data(), 1, 64, 64, 77, ec.data())) ||
+                (st = unet_forward_host(ctx->c, lat.data(), t999.data(), uc.data(), 1, 64, 64, 77, eu.data())))
+                return st;
+            double d = 0;
+            for (size_t i = 0; i < LAT; ++i) d += std::fabs(ec[i] - eu[i]);
+            out->ctx_sens = d / (double)LAT;
+        }
+        return SDU_OK;
+    });
+}
+
+double sdu_selftest(sdu_ctx* ctx, const char* fixture_dir) {
+    if (!ctx) return (double)SDU_ERR_NOT_INIT;
+    sdu_selftest_report r;
+    const int st = sdu_selftest_ex(ctx, fixture_dir, &r);
+    if (st) return (double)st;
+    return std::max(r.relerr_b1, std::max(r.relerr_b2[0], r.relerr_b2[1]));
+}
+
+int sdu_time_proj(int t, float* out) {
+    if (!out || t < 0 || t > 100000) return fail(nullptr, SDU_ERR_ARG, "bad time_proj argument");
+    time_proj_host(t, out);
+    return SDU_OK;
 }
 
 int sdu_profile(sdu_ctx* ctx, int B, int H, int W, int L, sdu_prof_entry* out, int max_entries,

@@ -106,7 +106,8 @@ struct Ctx {
     std::map<std::string, int> res_by_pf, xf_by_pf;
 
     // op-level tensors and per-shape forward state
-    std::vector<FwdState*> fwd;  // owned; freed by free_fwd_states
+    std::vector<FwdState*> fwd;  // owned; freed by free_fwd_states (LRU-capped)
+    uint64_t use_clock = 0;
     float* op_ws = nullptr;     // scratch for op-level calls
     size_t op_ws_bytes = 0;
 
@@ -152,6 +153,8 @@ int unet_denoise_device(Ctx& c, const float* d_lat, const float* d_cond, const f
                         int H, int W, int L, int steps, float guidance, int cfg_steps,
                         const float* d_noise, uint64_t noise_seed, float* d_out);
 int unet_profile(Ctx& c, int B, int H, int W, int L);
+// timeProj (VulkanUnetPipeline.kt:36-46): out[320] = [cos(t f_i) | sin(t f_i)]
+void time_proj_host(int t, float* out);
 void free_fwd_states(Ctx& c);
 
 }  // namespace sdu

@@ -588,11 +588,12 @@ void gemm_kernel(GemmArgs a) {
         // last block to arrive sums the slots and goes on to the epilogue; the others
         // are done.  No block waits for another.
         //
-        // The slot stores and loads are device-coherent (sc1: they bypass the
-        // per-XCD L2 state that plain accesses may leave stale or unwritten), and each
-        // wave's stores are complete (vmcnt 0) before the barrier that precedes the
-        // count, so a block that sees the final count reads every slot's final data
-        // without a full L2 write-back / invalidate.
+        // Ordering (HIP memory model, agent scope): every wave's slot stores precede the
+        // block barrier, the barrier precedes thread 0's release increment of the tile
+        // counter, and the last arriver's acquire of the counter precedes its barrier and
+        // the slot loads, so the loads see every slot.  The slot stores and loads are
+        // also device-coherent (sc1), so that they do not depend on the per-XCD L2
+        // write-back and invalidate of the release / acquire.
         constexpr int SLOT = MT * NT;       // floats per slot
         constexpr int CPOL_SC1 = 1 << 4;    // buffer cache policy: device-coherent
         typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -614,7 +615,7 @@ void gemm_kernel(GemmArgs a) {
         __syncthreads();        // ... for every wave; no wave still reads the ring
         int* const flag = (int*)smem;
         if (tid == 0) {
-            const unsigned prev = __hip_atomic_fetch_add(a.tile_cnt + bid, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const unsigned prev = __hip_atomic_fetch_add(a.tile_cnt + bid, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
             const bool last = prev == (unsigned)a.splits - 1;
             // ready for the next launch on this workspace
             if (last) __hip_atomic_store(a.tile_cnt + bid, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -622,6 +623,7 @@ void gemm_kernel(GemmArgs a) {
         }
         __syncthreads();
         if (!*flag) return;
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         // The tile is the sum of all slots in slot order (the own slot re-read), so
         // the result does not depend on which block arrived last.  Slots go in rounds
         // of SPR, every load of a round issued before any is added (slot indices

@@ -118,7 +118,8 @@ __global__ void lcm_step_kernel(float* x, const float* eps2, const float* noise,
     // host formulas, so the device loop reproduces a host loop bit for bit.
     // eps = u + s (c - u) in float32 (VulkanUnetPipeline.kt:86)
     const float ec = eps2[i];
-    const float eps = c.cond_only ? ec : __fadd_rn(eps2[n + i], __fmul_rn(c.guidance, __fsub_rn(ec, eps2[n + i])));
+    const float g = c.guidance_dev ? *c.guidance_dev : c.guidance;
+    const float eps = c.cond_only ? ec : __fadd_rn(eps2[n + i], __fmul_rn(g, __fsub_rn(ec, eps2[n + i])));
     // LcmScheduler.kt:70-79 in float64
     const double xv = (double)x[i];
     const double x0 = __ddiv_rn(__dsub_rn(xv, __dmul_rn(c.sqrt_beta, (double)eps)), c.sqrt_alpha);
@@ -141,6 +142,19 @@ hipError_t lcm_step_launch(float* x, const float* eps2, const float* noise, int6
     launch_timed("lcm_step_kernel", 0.0, 16.0 * n, [&] {
         hipLaunchKernelGGL(lcm_step_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, eps2,
                            noise, n, c, unet_in, C, HW, Cpad);
+    });
+    return hipGetLastError();
+}
+
+__global__ void fill_f32_kernel(float* p, float v, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+hipError_t fill_f32_launch(float* p, float v, int64_t n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    launch_timed("fill_f32_kernel", 0.0, 4.0 * n, [&] {
+        hipLaunchKernelGGL(fill_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p, v, n);
     });
     return hipGetLastError();
 }

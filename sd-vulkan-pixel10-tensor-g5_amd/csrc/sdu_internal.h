@@ -168,10 +168,13 @@ hipError_t geglu_launch(const f16* g, f16* y, int T, int C2, hipStream_t s);
 
 struct LcmCoeffs {
     float guidance;
+    const float* guidance_dev;  // if set, the guidance scale is read from device memory
     double sqrt_alpha, sqrt_beta, c_skip, c_out, sqrt_alpha_prev, sqrt_beta_prev;
     int last;
     int cond_only;  // eps = cond (a step without CFG: eps2 holds only the cond half)
 };
+// p[0, n) = v (graph-safe fill kernel)
+hipError_t fill_f32_launch(float* p, float v, int64_t n, hipStream_t s);
 // eps2: [2, n] (cond, uncond) fp32; x: [n] fp32 updated in place; noise [n] or null.
 // If unet_in != null, also writes the next UNet input NHWC fp16 [2, HW, Cpad]
 // (x duplicated into both CFG slots, C channels of HW pixels).

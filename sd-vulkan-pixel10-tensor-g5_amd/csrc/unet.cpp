@@ -31,12 +31,13 @@ struct ProfRec {
     hipEvent_t e0, e1;
 };
 
-// Times every kernel launch on its own: the launch is issued `reps` times back to
-// back between two events, so the per-launch figure is the steady-state duration
-// of that kernel on a busy stream, as in a graph replay.
+// Times every kernel launch on its own: the launch is issued `reps` times (default
+// once) between two events on the engine stream.  With one launch per kernel the
+// profiled pass computes the same values as a forward (in-place residual updates and
+// statistics accumulators are applied once); repeats drift them.
 struct EventTimer : KernelTimer {
     hipStream_t s;
-    int reps = 5;
+    int reps = 1;
     std::string cat, shape;
     std::vector<ProfRec> recs;
     void run(const char* kernel, double flops, double bytes, void (*fn)(const void*), const void* arg) override {
@@ -466,7 +467,7 @@ struct LcmSched {
 };
 
 // sinusoid of VulkanUnetPipeline.kt:36-46 in float64
-static void time_proj_host(int t, float* out) {
+void time_proj_host(int t, float* out) {
     for (int i = 0; i < 160; ++i) {
         const double a = t * std::exp(-std::log(10000.0) * i / 160.0);
         out[i] = (float)std::cos(a);
@@ -480,8 +481,12 @@ struct FwdState {
     int kind;  // 0 forward, 1 denoise
     Fwd f;
     int steps = 0;
-    float guidance = 0.f;
-    int cfg_steps = 0;  // denoise: steps [0, cfg_steps) run batch CFG, the rest cond only
+    // denoise: steps [0, cfg_steps) run batch CFG, the rest cond only (0 when the
+    // guidance scale is <= 1).  The scale itself is not part of the graph: the CFG
+    // combine reads it from d_guidance, written before each replay.
+    int cfg_steps = 0;
+    float* d_guidance = nullptr;
+    uint64_t last_use = 0;  // LRU order of the planned states
     char* arena = nullptr;
     size_t arena_bytes = 0;
     float* gemm_ws = nullptr;
@@ -521,13 +526,14 @@ static void body(Exec& E, FwdState& S) {
     for (int i = 0; i < S.steps; ++i) {
         // TpuUnetPipeline.kt:94-99: CFG on the first cfg_steps steps, then one forward on
         // cond alone (its image 0: slot 0 of the input, the first L rows of K/V)
-        const bool cfg = S.guidance > 1.f && i < S.cfg_steps;
+        const bool cfg = i < S.cfg_steps;
         E.B = cfg ? 2 : 1;
         Fwd Fi = F;
         Fi.B = E.B;
         unet_core(E, Fi, lat, S.in_temb + (size_t)i * 320, kv, eps2);
         E.B = 2;
-        LcmCoeffs co = sched.coeffs(i, S.guidance);
+        LcmCoeffs co = sched.coeffs(i, 0.f);
+        co.guidance_dev = S.d_guidance;
         co.cond_only = !cfg;
         const float* nz = co.last ? nullptr : S.in_noise + (size_t)i * n;
         f16* next = co.last ? nullptr : lat;
@@ -547,6 +553,7 @@ static void free_state(FwdState* S) {
     hipFree(S->in_ctx);
     hipFree(S->in_noise);
     hipFree(S->out);
+    hipFree(S->d_guidance);
 }
 
 void free_fwd_states(Ctx& c) {
@@ -585,6 +592,7 @@ static int plan_state(Ctx& c, FwdState& S) {
     if (S.kind == 1 && (e = mal((void**)&S.in_noise, (size_t)(S.steps > 1 ? S.steps - 1 : 1) * kLatC * HW * 4)) != hipSuccess)
         return set_err(&c, SDU_ERR_OOM, "staging");
     if ((e = mal((void**)&S.out, lat_n * 4)) != hipSuccess) return set_err(&c, SDU_ERR_OOM, "staging");
+    if (S.kind == 1 && (e = mal((void**)&S.d_guidance, 4)) != hipSuccess) return set_err(&c, SDU_ERR_OOM, "staging");
     if (S.kind == 1) {
         LcmSched sched(S.steps);
         std::vector<float> te((size_t)S.steps * 320);
@@ -612,20 +620,35 @@ static int plan_state(Ctx& c, FwdState& S) {
     return SDU_OK;
 }
 
-static FwdState* get_state(Ctx& c, int kind, int B, int H, int W, int L, int steps, float guidance,
-                           int cfg_steps, int* st) {
+// At most kMaxStates planned states (arena, workspace, staging and graph each) are
+// kept per context; planning another evicts the least recently used one.
+static const size_t kMaxStates = 16;
+
+static FwdState* get_state(Ctx& c, int kind, int B, int H, int W, int L, int steps, int cfg_steps, int* st) {
     for (FwdState* s : c.fwd)
         if (s->kind == kind && s->f.B == B && s->f.H == H && s->f.W == W && s->f.L == L &&
-            s->steps == steps && (kind == 0 || (s->guidance == guidance && s->cfg_steps == cfg_steps)))
+            s->steps == steps && s->cfg_steps == cfg_steps) {
+            s->last_use = ++c.use_clock;
             return s;
+        }
+    if (c.fwd.size() >= kMaxStates) {
+        // the evicted state's graph may still be running on the stream
+        hipError_t e = hipStreamSynchronize(c.stream);
+        if (e != hipSuccess) { *st = hip_fail(c, e, "evict state"); return nullptr; }
+        auto lru = std::min_element(c.fwd.begin(), c.fwd.end(),
+                                    [](const FwdState* a, const FwdState* b) { return a->last_use < b->last_use; });
+        free_state(*lru);
+        delete *lru;
+        c.fwd.erase(lru);
+    }
     std::unique_ptr<FwdState> S(new FwdState());
     S->kind = kind;
     S->f = Fwd{B, H, W, L};
     S->steps = steps;
-    S->guidance = guidance;
     S->cfg_steps = cfg_steps;
     *st = plan_state(c, *S);
     if (*st) { free_state(S.get()); return nullptr; }
+    S->last_use = ++c.use_clock;
     c.fwd.push_back(S.release());
     return c.fwd.back();
 }
@@ -641,7 +664,7 @@ int unet_forward_device(Ctx& c, const float* d_lat, const float* d_temb, const f
                         int W, int L, float* d_out) {
     int st = check_shape(c, B, H, W, L);
     if (st) return st;
-    FwdState* S = get_state(c, 0, B, H, W, L, 0, 0.f, 0, &st);
+    FwdState* S = get_state(c, 0, B, H, W, L, 0, 0, &st);
     if (!S) return st;
     const size_t lat_b = (size_t)B * kLatC * H * W * 4;
     hipError_t e;
@@ -658,7 +681,7 @@ int unet_forward_host(Ctx& c, const float* lat, const float* temb, const float* 
                       int L, float* out) {
     int st = check_shape(c, B, H, W, L);
     if (st) return st;
-    FwdState* S = get_state(c, 0, B, H, W, L, 0, 0.f, 0, &st);
+    FwdState* S = get_state(c, 0, B, H, W, L, 0, 0, &st);
     if (!S) return st;
     const size_t lat_b = (size_t)B * kLatC * H * W * 4;
     hipError_t e;
@@ -679,8 +702,9 @@ int unet_denoise_device(Ctx& c, const float* d_lat, const float* d_cond, const f
     if (st) return st;
     if (steps < 1 || steps > 50) return set_err(&c, SDU_ERR_ARG, "steps must be in 1..50");
     if (cfg_steps < 0 || cfg_steps > steps) return set_err(&c, SDU_ERR_ARG, "cfg_steps must be in 0..steps");
+    if (!std::isfinite(guidance)) return set_err(&c, SDU_ERR_ARG, "guidance must be finite");
     if (!(guidance > 1.f)) cfg_steps = 0;  // no CFG on any step (TpuUnetPipeline.kt:97)
-    FwdState* S = get_state(c, 1, 2, H, W, L, steps, guidance, cfg_steps, &st);
+    FwdState* S = get_state(c, 1, 2, H, W, L, steps, cfg_steps, &st);
     if (!S) return st;
     const size_t n = (size_t)kLatC * H * W;
     const size_t cb = (size_t)L * kCtxDim * 4;
@@ -697,21 +721,22 @@ int unet_denoise_device(Ctx& c, const float* d_lat, const float* d_cond, const f
                                             fnv1a64("lcm.noise") ^ splitmix64(noise_seed), c.stream);
         if (e != hipSuccess) return hip_fail(c, e, "denoise");
     }
-    if ((e = hipGraphLaunch(S->exec, c.stream)) ||
+    if ((e = fill_f32_launch(S->d_guidance, guidance, 1, c.stream)) ||
+        (e = hipGraphLaunch(S->exec, c.stream)) ||
         (e = hipMemcpyAsync(d_out, S->out, n * 4, hipMemcpyDeviceToDevice, c.stream)))
         return hip_fail(c, e, "denoise");
     return SDU_OK;
 }
 
 // Eager forward with every kernel timed on its own (unetProfile,
-// vk_engine.cpp:854-872).  Each launch is repeated SDU_PROFILE_REPS times (default
-// 5) between its two events; the recorded time is the per-launch average.  The
-// repeats recompute the same kernels on the same buffers, so the activations of
-// this pass are not meaningful; the next forward starts from its own inputs.
+// vk_engine.cpp:854-872): HIP events around each launch on the engine stream.
+// SDU_PROFILE_REPS (default 1) repeats each launch between its events and keeps the
+// average; repeats re-apply in-place updates, so with more than one the activations
+// of this pass drift (the next forward starts from its own inputs).
 int unet_profile(Ctx& c, int B, int H, int W, int L) {
     int st = check_shape(c, B, H, W, L);
     if (st) return st;
-    FwdState* S = get_state(c, 0, B, H, W, L, 0, 0.f, 0, &st);
+    FwdState* S = get_state(c, 0, B, H, W, L, 0, 0, &st);
     if (!S) return st;
     hipError_t e = hipStreamSynchronize(c.stream);
     if (e != hipSuccess) return hip_fail(c, e, "profile");

@@ -36,7 +36,7 @@ SDU_EPI_OUT_F32 = 0x2
 EXPORTS = [
     "sdu_init", "sdu_release", "sdu_last_error", "sdu_synchronize", "sdu_set_weight",
     "sdu_get_weight", "sdu_param_count", "sdu_forward", "sdu_forward_cfg", "sdu_denoise_lcm",
-    "sdu_forward_device", "sdu_denoise_lcm_device", "sdu_denoise_lcm_ex", "sdu_selftest", "sdu_profile",
+    "sdu_forward_device", "sdu_denoise_lcm_device", "sdu_denoise_lcm_ex", "sdu_selftest", "sdu_selftest_ex", "sdu_time_proj", "sdu_profile",
     "sdu_tensor_alloc", "sdu_tensor_free", "sdu_tensor_upload", "sdu_tensor_download",
     "sdu_tensor_device_ptr", "sdu_tensor_bytes", "sdu_groupnorm", "sdu_layernorm", "sdu_matmul",
     "sdu_conv2d", "sdu_attention", "sdu_geglu", "sdu_silu", "sdu_add", "sdu_add_bias",
@@ -48,6 +48,11 @@ class SduError(RuntimeError):
     def __init__(self, code: int, msg: str):
         super().__init__(f"sdu error {code}: {msg}")
         self.code = code
+
+
+class SelftestReport(ctypes.Structure):
+    _fields_ = [("relerr_b1", ctypes.c_double), ("relerr_b2", ctypes.c_double * 2),
+                ("ctx_sens", ctypes.c_double)]
 
 
 class ProfEntry(ctypes.Structure):
@@ -88,6 +93,8 @@ def load(path: str = LIB_PATH):
         "sdu_denoise_lcm_device": ([P, P, P, P, I, I, I, I, F, P, P], I),
         "sdu_denoise_lcm_ex": ([P, P, P, P, I, I, I, I, F, I, P, ctypes.c_uint64, P], I),
         "sdu_selftest": ([P, ctypes.c_char_p], ctypes.c_double),
+        "sdu_selftest_ex": ([P, ctypes.c_char_p, ctypes.POINTER(SelftestReport)], I),
+        "sdu_time_proj": ([I, P], I),
         "sdu_profile": ([P, I, I, I, I, P, I, ctypes.POINTER(I), ctypes.POINTER(ctypes.c_double)], I),
         "sdu_tensor_alloc": ([P, I, I, ctypes.POINTER(I64), ctypes.POINTER(P)], I),
         "sdu_tensor_free": ([P, P], I),
@@ -116,6 +123,15 @@ def load(path: str = LIB_PATH):
 
 def _ptr(a: Optional[np.ndarray]):
     return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def time_proj(t: int) -> np.ndarray:
+    """sdu_time_proj: the 320-d sinusoid timestep embedding (float32)."""
+    out = np.empty(320, np.float32)
+    st = load().sdu_time_proj(int(t), _ptr(out))
+    if st != SDU_OK:
+        raise SduError(st, load().sdu_last_error(None).decode())
+    return out
 
 
 class Tensor:
@@ -253,6 +269,13 @@ class Engine:
 
     def selftest(self, fixture_dir: str) -> float:
         return float(load().sdu_selftest(self.h, fixture_dir.encode()))
+
+    def selftest_report(self, fixture_dir: str) -> dict:
+        """sdu_selftest_ex: the B=1, B=2 and context-sensitivity legs."""
+        r = SelftestReport()
+        self._check(load().sdu_selftest_ex(self.h, fixture_dir.encode(), ctypes.byref(r)))
+        return {"relerr_b1": r.relerr_b1, "relerr_b2": (r.relerr_b2[0], r.relerr_b2[1]),
+                "ctx_sens": r.ctx_sens}
 
     def profile(self, B, H, W, L=77):
         arr = (ProfEntry * 128)()

@@ -50,3 +50,15 @@ def test_init_without_device_fails_cleanly():
     h = ctypes.c_void_p()
     assert lib.sdu_init(ctypes.byref(h), None, 0, 0) == sdu.SDU_ERR_DEVICE
     assert not h.value
+
+
+def test_time_proj_matches_oracle():
+    """sdu_time_proj (timeProj, VulkanUnetPipeline.kt:36-46) against the oracle's
+    closed form; host code, no device."""
+    import numpy as np
+    import sdu
+    from oracle import lcm
+    for t in (0, 1, 259, 499, 759, 999):
+        np.testing.assert_allclose(sdu.time_proj(t), lcm.time_proj(t), rtol=0, atol=1e-7)
+    lib = sdu.load()
+    assert lib.sdu_time_proj(-1, None) == sdu.SDU_ERR_ARG

@@ -220,17 +220,29 @@ def test_set_weight_refolds_layernorm(unet_engine, oracle_weights):
             unet_engine.set_weight(n, v)
 
 
-def test_forward_b16_matches_pairs(unet_engine):
-    """B=16 throughput batch: eight copies of one CFG pair must each reproduce the
-    B=2 result (per-image independence of every kernel; split-K factors differ
-    with M, so equality is to fp32 accumulation-order tolerance)."""
-    lat, temb, ctx = inputs(2, 64, 64, seed=16)
-    say("forward B=16 64x64")
-    y2 = unet_engine.forward(lat, temb, ctx)
-    y16 = unet_engine.forward(np.concatenate([lat] * 8), temb, np.concatenate([ctx] * 8))
+def test_forward_b16_matches_pairs(unet_engine, oracle_weights):
+    """B=16 throughput batch (8 prompts x CFG), every image with its own latent and
+    context: each pair of the B=16 output must reproduce a B=2 forward of that pair
+    alone (an index mix-up between images -- attention grid, cross-K/V rows b*L,
+    statistics slots -- would pull in another pair's data), and the first and last
+    pairs are compared with the oracle directly (vk_engine.cpp:542, :823-839)."""
+    lat, temb, ctx = inputs(16, 64, 64, seed=16)
+    say("forward B=16 64x64 (distinct pairs)")
+    y16 = unet_engine.forward(lat, temb, ctx)
+    assert np.isfinite(y16).all()
     for i in range(8):
-        e = rel_err_l1(y16[2 * i:2 * i + 2], y2)
-        say(f"B=16 pair {i} vs B=2: {e:.2e}")
+        sl = slice(2 * i, 2 * i + 2)
+        y2 = unet_engine.forward(lat[sl], temb, ctx[sl])
+        e = rel_err_l1(y16[sl], y2)
+        say(f"B=16 pair {i} vs its own B=2 forward: {e:.2e}")
+        assert e <= 1e-3
+        # and the pairs really differ from each other
+        if i:
+            assert rel_err_l1(y16[sl], y16[0:2]) > 0.1
+    for i in (0, 7):
+        sl = slice(2 * i, 2 * i + 2)
+        e = rel_err_l1(y16[sl], oracle_forward(oracle_weights, lat[sl], temb, ctx[sl]))
+        say(f"B=16 pair {i} vs oracle: {e:.3e}")
         assert e <= TOL
 
 
@@ -299,6 +311,38 @@ def test_denoise_cfg_first_steps(unet_engine):
     b = _denoise_ex(unet_engine, lat, cond, unc, steps, g, 0, noise)
     assert np.array_equal(a, b)
     assert rel_err_l1(a, full) > 1e-2  # and it is a different result
+
+
+def test_denoise_guidance_shares_one_graph(unet_engine):
+    """The guidance scale is read by the denoise graph from device memory, so every
+    value > 1 replays the same graph: after a run at 8.0, a run at 3.0 equals the host
+    loop at 3.0 bit for bit, and sweeping many values allocates nothing new.  A NaN or
+    infinite guidance is rejected."""
+    import sdu
+    steps, H, W = 4, 32, 32
+    lat, cond, unc, noise = _denoise_inputs(H, W, steps)
+    _denoise_ex(unet_engine, lat, cond, unc, steps, 8.0, steps, noise)
+    g = 3.0
+    dev = _denoise_ex(unet_engine, lat, cond, unc, steps, g, steps, noise)
+    sched = lcm.LcmSchedule(steps)
+    x = lat.copy()
+    for idx, tt in enumerate(sched.timesteps):
+        both = unet_engine.forward_cfg(x, lcm.time_proj(tt), cond, unc)
+        eps = lcm.cfg_combine(both[0], both[1], g)
+        x = sched.step(idx, x, eps, None if idx == steps - 1 else noise[idx])
+    assert np.array_equal(dev, x)
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    for gg in np.linspace(1.5, 12.0, 12):
+        _denoise_ex(unet_engine, lat, cond, unc, steps, float(gg), steps, noise)
+    torch.cuda.synchronize()
+    grown = free0 - torch.cuda.mem_get_info()[0]
+    say(f"device memory taken by 12 more guidance values: {grown / 2**20:.1f} MiB")
+    assert grown < 64 * 2**20
+    for bad in (float("nan"), float("inf")):
+        with pytest.raises(sdu.SduError) as ex:
+            _denoise_ex(unet_engine, lat, cond, unc, steps, bad, steps, noise)
+        assert ex.value.code == sdu.SDU_ERR_ARG
 
 
 def test_denoise_device_noise(unet_engine):
@@ -410,6 +454,7 @@ def test_weights_dir_loader(tmp_path, unet_engine):
 
 def test_selftest_protocol(tmp_path, unet_engine, oracle_weights):
     """unetSelfTest (vk_engine.cpp:811-851) with fixtures written by the oracle."""
+    import sdu
     lat, temb, ctx = inputs(1, 64, 64, seed=19)
     lat16 = lat.astype(np.float16)
     ctx16 = ctx.astype(np.float16)
@@ -425,3 +470,23 @@ def test_selftest_protocol(tmp_path, unet_engine, oracle_weights):
     say(f"selftest relErr = {e:.3e}")
     assert 0 <= e <= TOL
     assert unet_engine.selftest(str(tmp_path / "missing")) < 0
+    r = unet_engine.selftest_report(d)
+    assert max(r["relerr_b1"], *r["relerr_b2"]) == e and r["ctx_sens"] == -1.0
+    # context-sensitivity leg (vk_engine.cpp:840-849): IN_cond / IN_unc at IN_temb999,
+    # mean |eps_cond - eps_unc| of two B=1 forwards, against the oracle's value
+    cond = Wt.gauss("input.cond", (77, 768), 19, fp16=True)
+    unc = Wt.gauss("input.uncond", (77, 768), 19, fp16=True)
+    t999 = lcm.time_proj(999).astype(np.float16)
+    cond.astype(np.float16).tofile(os.path.join(d, "IN_cond.bin"))
+    unc.astype(np.float16).tofile(os.path.join(d, "IN_unc.bin"))
+    t999.tofile(os.path.join(d, "IN_temb999.bin"))
+    ec = oracle_forward(oracle_weights, lat16.astype(np.float32), t999.astype(np.float32), cond[None])
+    eu = oracle_forward(oracle_weights, lat16.astype(np.float32), t999.astype(np.float32), unc[None])
+    d_ref = float(np.abs(ec - eu).mean())
+    r = unet_engine.selftest_report(d)
+    say(f"ctx sensitivity engine {r['ctx_sens']:.4e} oracle {d_ref:.4e}")
+    assert d_ref > 0 and abs(r["ctx_sens"] - d_ref) / d_ref < 0.05
+    # a context-sensitivity set with a short file is an error, not a silent zero
+    np.zeros(3, np.float16).tofile(os.path.join(d, "IN_unc.bin"))
+    with pytest.raises(sdu.SduError):
+        unet_engine.selftest_report(d)
