@@ -216,8 +216,8 @@ def main():
                 "frac": round(ach / PEAK_HBM_GBS, 4)}
     traffic = measured_traffic(dom_name)
     roof.update({"traffic": traffic, "kernel": dom_name, "calls": dom["calls"],
-                 "timing": "HIP events around each launch (one launch each) on the engine stream, "
-                           "eager profiling forward",
+                 "timing": "start/stop HIP events of each launch (hipExtLaunchKernelGGL) on the engine "
+                           "stream, one eager forward, each kernel once",
                  "flops_per_launch": dom["flops"] / dom["calls"],
                  "bytes_per_launch": dom["bytes"] / dom["calls"],
                  "avg_launch_us": round(avg_us, 3)})

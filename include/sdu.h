@@ -148,11 +148,10 @@ typedef struct sdu_selftest_report {
 int sdu_selftest_ex(sdu_ctx* ctx, const char* fixture_dir, sdu_selftest_report* out);
 
 /* unetProfile (vk_engine.cpp:854-872): one eager forward in which every kernel
- * launch is timed on its own with HIP events on the context stream (each launch once
- * between its events; the environment variable SDU_PROFILE_REPS > 1 repeats it and
- * keeps the average, at the cost of meaningless activations in that pass).  Entries
- * are accumulated per op category (e.g. "conv3x3") and per kernel ("k:" + kernel
- * name, e.g. "k:gemm_kernel<128,128,2,2,64,2>"); total_ms sums the categories. */
+ * launch is timed on its own: it carries a start and a stop HIP event that record the
+ * kernel's own execution on the context stream (hipExtLaunchKernelGGL), and runs once.
+ * Entries are accumulated per op category (e.g. "conv3x3") and per kernel ("k:" +
+ * kernel name, e.g. "k:gemm_kernel<128,128,2,2,64,2>"); total_ms sums the categories. */
 typedef struct sdu_prof_entry {
     char name[48];
     int calls;

@@ -59,6 +59,21 @@ int op_gemm(sdu_ctx* ctx, const GemmArgs& g, const char* what) {
     return finish(ctx, e, what);
 }
 
+// Shape and size checks of sdu_groupnorm.
+int gn_check(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* x2, const sdu_tensor* gamma,
+             const sdu_tensor* beta, const sdu_tensor* y, int B, int HW, int C1, int C2, int groups) {
+    const int C = C1 + C2;
+    if (B < 1 || B > 64 || HW < 1 || C1 < 8 || C2 < 0 || groups < 1 || groups > 32 || C % groups ||
+        C1 % 8 || C2 % 8 || (C2 && !x2))
+        return fail(ctx, SDU_ERR_ARG, "bad groupnorm shape");
+    const size_t px = (size_t)B * HW;
+    if (!fits(x, px * C1 * 2) || (C2 && !fits(x2, px * C2 * 2)) || !fits(gamma, (size_t)C * 2) ||
+        !fits(beta, (size_t)C * 2) || !fits(y, px * C * 2))
+        return fail(ctx, SDU_ERR_ARG, "groupnorm tensor too small");
+    if (C > 2560) return fail(ctx, SDU_ERR_ARG, "groupnorm supports C <= 2560");
+    return SDU_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -410,17 +425,10 @@ int sdu_groupnorm(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* x2, const
                   const sdu_tensor* beta, sdu_tensor* y, int B, int HW, int C1, int C2, int groups,
                   float eps, int silu) {
     SDU_GUARD(ctx);
-    const int C = C1 + C2;
-    if (B < 1 || B > 64 || HW < 1 || C1 < 8 || C2 < 0 || groups < 1 || groups > 32 || C % groups ||
-        C1 % 8 || C2 % 8 || (C2 && !x2))
-        return fail(ctx, SDU_ERR_ARG, "bad groupnorm shape");
-    const size_t px = (size_t)B * HW;
-    if (!fits(x, px * C1 * 2) || (C2 && !fits(x2, px * C2 * 2)) || !fits(gamma, (size_t)C * 2) ||
-        !fits(beta, (size_t)C * 2) || !fits(y, px * C * 2))
-        return fail(ctx, SDU_ERR_ARG, "groupnorm tensor too small");
-    if (C > 2560) return fail(ctx, SDU_ERR_ARG, "groupnorm supports C <= 2560");
+    int st = gn_check(ctx, x, x2, gamma, beta, y, B, HW, C1, C2, groups);
+    if (st) return st;
     const size_t acc = groupnorm_acc_bytes(B, groups);
-    int st = ensure_op_ws(ctx->c, acc);
+    st = ensure_op_ws(ctx->c, acc);
     if (st) return st;
     hipError_t e = zero_launch(ctx->c.op_ws, acc, ctx->c.stream);
     if (e == hipSuccess)

@@ -484,8 +484,8 @@ static void launch_cfg(const AttnArgs& a, hipStream_t s) {
         snprintf(name, sizeof name, "attn_kernel<%d,%d,%d,%d>", KS, MTD, nw, (int)LSUM);
         const dim3 grid((a.Sq + nw * 32 - 1) / (nw * 32), a.heads, a.B);
         launch_timed(name, flops, bytes, [&] {
-            if (nw == 4) hipLaunchKernelGGL((attn_kernel<KS, MTD, 4, LSUM>), grid, dim3(256), 0, s, a);
-            else hipLaunchKernelGGL((attn_kernel<KS, MTD, 2, LSUM>), grid, dim3(128), 0, s, a);
+            if (nw == 4) SDU_LAUNCH((attn_kernel<KS, MTD, 4, LSUM>), grid, dim3(256), 0, s, a);
+            else SDU_LAUNCH((attn_kernel<KS, MTD, 2, LSUM>), grid, dim3(128), 0, s, a);
         });
         return;
     }
@@ -499,10 +499,10 @@ static void launch_cfg(const AttnArgs& a, hipStream_t s) {
     snprintf(name, sizeof name, "attn_split_kernel<%d,%d,%d,%d>", KS, MTD, ns, (int)LSUM);
     const dim3 grid((a.Sq + 31) / 32, a.heads, a.B);
     launch_timed(name, flops, bytes, [&] {
-        if (ns == 1) hipLaunchKernelGGL((attn_split_kernel<KS, MTD, 1, LSUM>), grid, dim3(64), 0, s, a);
-        else if (ns == 2) hipLaunchKernelGGL((attn_split_kernel<KS, MTD, 2, LSUM>), grid, dim3(128), 0, s, a);
-        else if (ns == 4) hipLaunchKernelGGL((attn_split_kernel<KS, MTD, 4, LSUM>), grid, dim3(256), 0, s, a);
-        else hipLaunchKernelGGL((attn_split_kernel<KS, MTD, (MTD > 3 ? 4 : 8), LSUM>), grid,
+        if (ns == 1) SDU_LAUNCH((attn_split_kernel<KS, MTD, 1, LSUM>), grid, dim3(64), 0, s, a);
+        else if (ns == 2) SDU_LAUNCH((attn_split_kernel<KS, MTD, 2, LSUM>), grid, dim3(128), 0, s, a);
+        else if (ns == 4) SDU_LAUNCH((attn_split_kernel<KS, MTD, 4, LSUM>), grid, dim3(256), 0, s, a);
+        else SDU_LAUNCH((attn_split_kernel<KS, MTD, (MTD > 3 ? 4 : 8), LSUM>), grid,
                                 dim3(64 * (MTD > 3 ? 4 : 8)), 0, s, a);
     });
 }

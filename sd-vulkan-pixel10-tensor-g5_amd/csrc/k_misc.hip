@@ -31,7 +31,7 @@ hipError_t nchw_to_nhwc_launch(const float* src, f16* dst, int B, int Bsrc, int 
                                hipStream_t s) {
     const int64_t total = (int64_t)B * HW * Cpad;
     launch_timed("nchw_to_nhwc_kernel", 0.0, 4.0 * Bsrc * C * HW + 2.0 * total, [&] {
-        hipLaunchKernelGGL(nchw_to_nhwc_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+        SDU_LAUNCH(nchw_to_nhwc_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
                            src, dst, B, Bsrc, C, Cpad, HW);
     });
     return hipGetLastError();
@@ -47,13 +47,13 @@ __global__ void f16_to_f32_kernel(const f16* src, float* dst, int64_t n) {
 }
 hipError_t f32_to_f16_launch(const float* src, f16* dst, int64_t n, hipStream_t s) {
     launch_timed("f32_to_f16_kernel", 0.0, 6.0 * n, [&] {
-        hipLaunchKernelGGL(f32_to_f16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src, dst, n);
+        SDU_LAUNCH(f32_to_f16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src, dst, n);
     });
     return hipGetLastError();
 }
 hipError_t f16_to_f32_launch(const f16* src, float* dst, int64_t n, hipStream_t s) {
     launch_timed("f16_to_f32_kernel", 0.0, 6.0 * n, [&] {
-        hipLaunchKernelGGL(f16_to_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src, dst, n);
+        SDU_LAUNCH(f16_to_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src, dst, n);
     });
     return hipGetLastError();
 }
@@ -91,20 +91,20 @@ __global__ void geglu_kernel(const f16* g, f16* y, int T, int C2) {
 }
 
 hipError_t silu_launch(const f16* x, f16* y, int64_t n, hipStream_t s) {
-    hipLaunchKernelGGL(silu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, y, n);
+    SDU_LAUNCH(silu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, y, n);
     return hipGetLastError();
 }
 hipError_t add_launch(const f16* a, const f16* b, f16* y, int64_t n, hipStream_t s) {
-    hipLaunchKernelGGL(add_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a, b, y, n);
+    SDU_LAUNCH(add_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a, b, y, n);
     return hipGetLastError();
 }
 hipError_t add_bias_launch(f16* y, const f16* bias, int64_t n, int C, hipStream_t s) {
-    hipLaunchKernelGGL(add_bias_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, y, bias, n, C);
+    SDU_LAUNCH(add_bias_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, y, bias, n, C);
     return hipGetLastError();
 }
 hipError_t geglu_launch(const f16* g, f16* y, int T, int C2, hipStream_t s) {
     const int64_t n = (int64_t)T * C2;
-    hipLaunchKernelGGL(geglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, g, y, T, C2);
+    SDU_LAUNCH(geglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, g, y, T, C2);
     return hipGetLastError();
 }
 
@@ -112,21 +112,35 @@ hipError_t geglu_launch(const f16* g, f16* y, int T, int C2, hipStream_t s) {
 
 __global__ void lcm_step_kernel(float* x, const float* eps2, const float* noise, int64_t n,
                                 LcmCoeffs c, f16* unet_in, int C, int HW, int Cpad) {
+    // Every operation rounds separately, in the order of the host formulas, so the device
+    // loop reproduces a host loop bit for bit: contraction into FMAs is off for the
+    // expressions below (a fused u + s (c - u) differs whenever s (c - u) is inexact).
+#pragma clang fp contract(off)
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    // Every operation rounds separately (no FMA contraction), in the order of the
-    // host formulas, so the device loop reproduces a host loop bit for bit.
     // eps = u + s (c - u) in float32 (VulkanUnetPipeline.kt:86)
     const float ec = eps2[i];
     const float g = c.guidance_dev ? *c.guidance_dev : c.guidance;
-    const float eps = c.cond_only ? ec : __fadd_rn(eps2[n + i], __fmul_rn(g, __fsub_rn(ec, eps2[n + i])));
+    float eps = ec;
+    if (!c.cond_only) {
+        const float eu = eps2[n + i];
+        const float d = ec - eu;
+        const float sd = g * d;
+        eps = eu + sd;
+    }
     // LcmScheduler.kt:70-79 in float64
     const double xv = (double)x[i];
-    const double x0 = __ddiv_rn(__dsub_rn(xv, __dmul_rn(c.sqrt_beta, (double)eps)), c.sqrt_alpha);
-    const double den = __dadd_rn(__dmul_rn(c.c_out, x0), __dmul_rn(c.c_skip, xv));
+    const double be = c.sqrt_beta * (double)eps;
+    const double x0 = (xv - be) / c.sqrt_alpha;
+    const double t0 = c.c_out * x0, t1 = c.c_skip * xv;
+    const double den = t0 + t1;
     float out;
-    if (c.last) out = (float)den;
-    else out = (float)__dadd_rn(__dmul_rn(c.sqrt_alpha_prev, den), __dmul_rn(c.sqrt_beta_prev, (double)noise[i]));
+    if (c.last) {
+        out = (float)den;
+    } else {
+        const double u0 = c.sqrt_alpha_prev * den, u1 = c.sqrt_beta_prev * (double)noise[i];
+        out = (float)(u0 + u1);
+    }
     x[i] = out;
     if (unet_in) {
         // i indexes the NCHW latent [C, HW]; write NHWC [2, HW, Cpad] for both slots
@@ -140,7 +154,7 @@ __global__ void lcm_step_kernel(float* x, const float* eps2, const float* noise,
 hipError_t lcm_step_launch(float* x, const float* eps2, const float* noise, int64_t n, LcmCoeffs c,
                            f16* unet_in, int C, int HW, int Cpad, hipStream_t s) {
     launch_timed("lcm_step_kernel", 0.0, 16.0 * n, [&] {
-        hipLaunchKernelGGL(lcm_step_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, eps2,
+        SDU_LAUNCH(lcm_step_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, eps2,
                            noise, n, c, unet_in, C, HW, Cpad);
     });
     return hipGetLastError();
@@ -154,7 +168,7 @@ __global__ void fill_f32_kernel(float* p, float v, int64_t n) {
 hipError_t fill_f32_launch(float* p, float v, int64_t n, hipStream_t s) {
     if (n <= 0) return hipSuccess;
     launch_timed("fill_f32_kernel", 0.0, 4.0 * n, [&] {
-        hipLaunchKernelGGL(fill_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p, v, n);
+        SDU_LAUNCH(fill_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p, v, n);
     });
     return hipGetLastError();
 }
@@ -223,13 +237,13 @@ __global__ void gen_normal_f32_kernel(float* dst, int64_t n, uint64_t key) {
 hipError_t gen_normal_f32_launch(float* dst, int64_t n, uint64_t key, hipStream_t s) {
     if (n <= 0) return hipSuccess;
     launch_timed("gen_normal_f32_kernel", 0.0, 4.0 * n, [&] {
-        hipLaunchKernelGGL(gen_normal_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, dst, n, key);
+        SDU_LAUNCH(gen_normal_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, dst, n, key);
     });
     return hipGetLastError();
 }
 
 hipError_t gen_launch(f16* dst, const GenDesc& g, hipStream_t s) {
-    hipLaunchKernelGGL(gen_kernel, dim3((unsigned)((g.n + 255) / 256)), dim3(256), 0, s, dst, g);
+    SDU_LAUNCH(gen_kernel, dim3((unsigned)((g.n + 255) / 256)), dim3(256), 0, s, dst, g);
     return hipGetLastError();
 }
 
@@ -306,9 +320,9 @@ __global__ void fold_ffout_bias_kernel(const f16* Wp, const f16* bf, const f16* 
 hipError_t fold_ffout_launch(const f16* Wp, const f16* bp, const f16* Wf, const f16* bf, f16* wcat, f16* bcat,
                              int C, hipStream_t s) {
     if (C <= 0 || C % 16) return hipErrorInvalidValue;  // 4C: whole 64-column tiles
-    hipLaunchKernelGGL(fold_ffout_kernel, dim3((5 * C + FT - 1) / FT, (C + FT - 1) / FT), dim3(256), 0, s, Wp, Wf,
+    SDU_LAUNCH(fold_ffout_kernel, dim3((5 * C + FT - 1) / FT, (C + FT - 1) / FT), dim3(256), 0, s, Wp, Wf,
                        wcat, C);
-    hipLaunchKernelGGL(fold_ffout_bias_kernel, dim3((C + 255) / 256), dim3(256), 0, s, Wp, bf, bp, bcat, C);
+    SDU_LAUNCH(fold_ffout_bias_kernel, dim3((C + 255) / 256), dim3(256), 0, s, Wp, bf, bp, bcat, C);
     return hipGetLastError();
 }
 
@@ -326,7 +340,7 @@ __global__ void fold_shortcut_kernel(const f16* w2, const f16* b2, const f16* ws
 hipError_t fold_shortcut_launch(const f16* w2, const f16* b2, const f16* ws, const f16* bs, f16* wcat, f16* bcat,
                                 int Co, int Ci2, int Cs, hipStream_t s) {
     if (Co <= 0 || Ci2 <= 0 || Cs <= 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(fold_shortcut_kernel, dim3(8, Co), dim3(256), 0, s, w2, b2, ws, bs, wcat, bcat, Co, 9 * Ci2, Cs);
+    SDU_LAUNCH(fold_shortcut_kernel, dim3(8, Co), dim3(256), 0, s, w2, b2, ws, bs, wcat, bcat, Co, 9 * Ci2, Cs);
     return hipGetLastError();
 }
 
@@ -360,7 +374,7 @@ __global__ __launch_bounds__(256) void fold_ln_kernel(const f16* W, const f16* b
 hipError_t fold_ln_launch(const f16* W, const f16* b, const f16* gamma, const f16* beta, f16* Wf, float* bf,
                           float* sf, int N, int K, hipStream_t s) {
     if (N <= 0 || K <= 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(fold_ln_kernel, dim3(N), dim3(256), 0, s, W, b, gamma, beta, Wf, bf, sf, K);
+    SDU_LAUNCH(fold_ln_kernel, dim3(N), dim3(256), 0, s, W, b, gamma, beta, Wf, bf, sf, K);
     return hipGetLastError();
 }
 

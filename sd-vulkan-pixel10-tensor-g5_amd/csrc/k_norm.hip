@@ -387,7 +387,7 @@ hipError_t zero_launch(void* p, size_t bytes, hipStream_t s) {
     const int64_t n16 = (int64_t)((bytes + 15) / 16);
     if (n16 == 0) return hipSuccess;
     launch_timed("zero_kernel", 0.0, 16.0 * n16, [&] {
-        hipLaunchKernelGGL(zero_kernel, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0, s, (uint4*)p, n16);
+        SDU_LAUNCH(zero_kernel, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0, s, (uint4*)p, n16);
     });
     return hipGetLastError();
 }
@@ -414,7 +414,7 @@ hipError_t groupnorm_launch(const f16* x, const f16* x2, int C1, int C2, const f
         const dim3 grid(G, B);
         launch_timed(name, 0.0, 2.0 * xbytes, [&] {
 #define GNF_LAUNCH(EPV, VWV)                                                                                 \
-    hipLaunchKernelGGL((gn_fused_kernel<EPV, VWV>), grid, dim3(GNF_THREADS), 0, s, x, x2, C1, C2, gamma, beta, y, \
+    SDU_LAUNCH((gn_fused_kernel<EPV, VWV>), grid, dim3(GNF_THREADS), 0, s, x, x2, C1, C2, gamma, beta, y, \
                        B, HW, G, eps, silu)
 #define GNF_VW(EPV)                      \
     if (vw == 8) GNF_LAUNCH(EPV, 8);     \
@@ -431,14 +431,14 @@ hipError_t groupnorm_launch(const f16* x, const f16* x2, int C1, int C2, const f
     }
     GnGeom g = gn_geom(HW, C);
     launch_timed("gn_stats_kernel", 0.0, xbytes, [&] {
-        hipLaunchKernelGGL(gn_stats_kernel, dim3(g.nchunk, B), dim3(GN_THREADS), 0, s, x, x2, C1, C2, HW,
+        SDU_LAUNCH(gn_stats_kernel, dim3(g.nchunk, B), dim3(GN_THREADS), 0, s, x, x2, C1, C2, HW,
                            g.P, G, acc);
     });
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const dim3 agrid(gna_blocks(HW, C, B), B);
     launch_timed("gn_apply_kernel<0>", 0.0, 2.0 * xbytes, [&] {
-        hipLaunchKernelGGL(gn_apply_kernel<false>, agrid, dim3(GN_THREADS), 0, s, x, x2, C1, C2, gamma, beta, y,
+        SDU_LAUNCH(gn_apply_kernel<false>, agrid, dim3(GN_THREADS), 0, s, x, x2, C1, C2, gamma, beta, y,
                            HW, G, eps, silu, (const double*)acc, (const double*)nullptr);
     });
     return hipGetLastError();
@@ -454,7 +454,7 @@ hipError_t groupnorm_apply_stats_launch(const f16* x, const f16* x2, int C1, int
     const double xbytes = 2.0 * B * HW * C;
     const dim3 agrid(gna_blocks(HW, C, B), B);
     launch_timed("gn_apply_kernel<1>", 0.0, 2.0 * xbytes, [&] {
-        hipLaunchKernelGGL(gn_apply_kernel<true>, agrid, dim3(GN_THREADS), 0, s, x, x2, C1, C2, gamma, beta, y, HW,
+        SDU_LAUNCH(gn_apply_kernel<true>, agrid, dim3(GN_THREADS), 0, s, x, x2, C1, C2, gamma, beta, y, HW,
                            G, eps, silu, st1, st2);
     });
     return hipGetLastError();
@@ -519,10 +519,10 @@ hipError_t layernorm_launch(const f16* x, const f16* gamma, const f16* beta, f16
     static const char* kNames[4] = {"ln_kernel<1>", "ln_kernel<2>", "ln_kernel<3>", "ln_kernel<4>"};
     const int v = C <= 512 ? 0 : C <= 1024 ? 1 : C <= 1536 ? 2 : 3;
     launch_timed(kNames[v], 0.0, 4.0 * T * C, [&] {
-        if (v == 0) hipLaunchKernelGGL(ln_kernel<1>, grid, block, 0, s, x, gamma, beta, y, T, C, eps);
-        else if (v == 1) hipLaunchKernelGGL(ln_kernel<2>, grid, block, 0, s, x, gamma, beta, y, T, C, eps);
-        else if (v == 2) hipLaunchKernelGGL(ln_kernel<3>, grid, block, 0, s, x, gamma, beta, y, T, C, eps);
-        else hipLaunchKernelGGL(ln_kernel<4>, grid, block, 0, s, x, gamma, beta, y, T, C, eps);
+        if (v == 0) SDU_LAUNCH(ln_kernel<1>, grid, block, 0, s, x, gamma, beta, y, T, C, eps);
+        else if (v == 1) SDU_LAUNCH(ln_kernel<2>, grid, block, 0, s, x, gamma, beta, y, T, C, eps);
+        else if (v == 2) SDU_LAUNCH(ln_kernel<3>, grid, block, 0, s, x, gamma, beta, y, T, C, eps);
+        else SDU_LAUNCH(ln_kernel<4>, grid, block, 0, s, x, gamma, beta, y, T, C, eps);
     });
     return hipGetLastError();
 }

@@ -3,6 +3,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <hip/hip_fp16.h>
 
 #include <cstdint>
@@ -34,6 +35,20 @@ struct KernelTimer {
                      const void* arg) = 0;
 };
 extern thread_local KernelTimer* g_kernel_timer;
+
+// Start / stop events of the launch the eager profiler is timing (null otherwise).
+// Every kernel is launched through SDU_LAUNCH: while these are set it goes through
+// hipExtLaunchKernelGGL, whose events record the start and end of that kernel's own
+// execution on the stream (no marker packets around it); otherwise it is a plain launch.
+extern thread_local hipEvent_t g_launch_ev0, g_launch_ev1;
+#define SDU_LAUNCH(kern, grid, block, shm, stream, ...)                                               \
+    do {                                                                                              \
+        if (::sdu::g_launch_ev0)                                                                     \
+            hipExtLaunchKernelGGL(kern, grid, block, shm, stream, ::sdu::g_launch_ev0, ::sdu::g_launch_ev1, 0, \
+                                  __VA_ARGS__);                                                       \
+        else                                                                                          \
+            hipLaunchKernelGGL(kern, grid, block, shm, stream, __VA_ARGS__);                          \
+    } while (0)
 
 template <class F>
 inline void launch_timed(const char* kernel, double flops, double bytes, const F& f) {

@@ -23,32 +23,32 @@ static const int kLatC = 4, kLatCpad = 8, kCtxDim = 768;
 // ------------------------------------------------------------------ execution
 
 thread_local KernelTimer* g_kernel_timer = nullptr;
+thread_local hipEvent_t g_launch_ev0 = nullptr, g_launch_ev1 = nullptr;
 
 struct ProfRec {
     std::string cat, kern, shape;
     double flops, bytes;
-    int reps;
     hipEvent_t e0, e1;
 };
 
-// Times every kernel launch on its own: the launch is issued `reps` times (default
-// once) between two events on the engine stream.  With one launch per kernel the
-// profiled pass computes the same values as a forward (in-place residual updates and
-// statistics accumulators are applied once); repeats drift them.
+// Times every kernel launch on its own: the launch goes through hipExtLaunchKernelGGL
+// with a start and a stop event of its own (SDU_LAUNCH), which record the start and end
+// of that kernel's execution.  Each kernel runs once, so the profiled pass computes the
+// same values as a forward.
 struct EventTimer : KernelTimer {
     hipStream_t s;
-    int reps = 1;
     std::string cat, shape;
     std::vector<ProfRec> recs;
     void run(const char* kernel, double flops, double bytes, void (*fn)(const void*), const void* arg) override {
         ProfRec pr;
         pr.cat = cat; pr.kern = kernel; pr.shape = shape;
-        pr.flops = flops; pr.bytes = bytes; pr.reps = reps;
+        pr.flops = flops; pr.bytes = bytes;
         hipEventCreate(&pr.e0);
         hipEventCreate(&pr.e1);
-        hipEventRecord(pr.e0, s);
-        for (int r = 0; r < reps; ++r) fn(arg);
-        hipEventRecord(pr.e1, s);
+        g_launch_ev0 = pr.e0;
+        g_launch_ev1 = pr.e1;
+        fn(arg);
+        g_launch_ev0 = g_launch_ev1 = nullptr;
         recs.push_back(pr);
     }
 };
@@ -729,10 +729,8 @@ int unet_denoise_device(Ctx& c, const float* d_lat, const float* d_cond, const f
 }
 
 // Eager forward with every kernel timed on its own (unetProfile,
-// vk_engine.cpp:854-872): HIP events around each launch on the engine stream.
-// SDU_PROFILE_REPS (default 1) repeats each launch between its events and keeps the
-// average; repeats re-apply in-place updates, so with more than one the activations
-// of this pass drift (the next forward starts from its own inputs).
+// vk_engine.cpp:854-872): each launch carries its own start / stop events
+// (hipExtLaunchKernelGGL on the engine stream) and runs once.
 int unet_profile(Ctx& c, int B, int H, int W, int L) {
     int st = check_shape(c, B, H, W, L);
     if (st) return st;
@@ -745,7 +743,6 @@ int unet_profile(Ctx& c, int B, int H, int W, int L) {
     ar.cap = S->arena_bytes;
     EventTimer timer;
     timer.s = c.stream;
-    if (const char* r = getenv("SDU_PROFILE_REPS")) timer.reps = std::min(100, std::max(1, atoi(r)));
     Exec E{c, c.stream, &ar, B};
     E.gemm_ws = S->gemm_ws;
     E.timer = &timer;
@@ -769,7 +766,6 @@ int unet_profile(Ctx& c, int B, int H, int W, int L) {
     for (ProfRec& r : timer.recs) {
         float ms = 0.f;
         if (e == hipSuccess) hipEventElapsedTime(&ms, r.e0, r.e1);
-        ms /= (float)r.reps;
         hipEventDestroy(r.e0);
         hipEventDestroy(r.e1);
         if (dump) fprintf(dump, "%s,\"%s\",\"%s\",%.0f,%.0f,%.5f\n", r.cat.c_str(), r.kern.c_str(), r.shape.c_str(),

@@ -235,7 +235,7 @@ def test_forward_b16_matches_pairs(unet_engine, oracle_weights):
         y2 = unet_engine.forward(lat[sl], temb, ctx[sl])
         e = rel_err_l1(y16[sl], y2)
         say(f"B=16 pair {i} vs its own B=2 forward: {e:.2e}")
-        assert e <= 1e-3
+        assert e <= TOL  # tile / split-K plans differ with M: fp16 rounding differs
         # and the pairs really differ from each other
         if i:
             assert rel_err_l1(y16[sl], y16[0:2]) > 0.1
