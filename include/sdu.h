@@ -184,6 +184,18 @@ int sdu_groupnorm(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* x2, const
                   const sdu_tensor* beta, sdu_tensor* y, int B, int HW, int C1, int C2,
                   int groups, float eps, int silu);
 
+/* sdu_groupnorm without any device allocation.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  Same arguments and results as
+ * sdu_groupnorm, but the statistics accumulators live in a fixed 32 KiB device array of
+ * the library (B <= 64 images x groups <= 32; larger is SDU_ERR_ARG) instead of the
+ * context's allocated workspace, and the call makes no hipMalloc / hipFree.  Every call
+ * on one device shares that array (cleared by a fill kernel at the start of each call):
+ * calls that overlap on one device, from several streams or contexts, race. */
+int sdu_groupnorm_noalloc(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* x2,
+                          const sdu_tensor* gamma, const sdu_tensor* beta, sdu_tensor* y, int B,
+                          int HW, int C1, int C2, int groups, float eps, int silu);
+
 /* LN (vk_engine.cpp:652): y[t,:] = LN(x[t,:]) over C. */
 int sdu_layernorm(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* gamma, const sdu_tensor* beta,
                   sdu_tensor* y, int T, int C, float eps);

@@ -6,6 +6,7 @@
 #include <cstdio>
 #include <cstring>
 #include <fstream>
+#include <mutex>
 #include <new>
 
 using namespace sdu;
@@ -59,7 +60,38 @@ int op_gemm(sdu_ctx* ctx, const GemmArgs& g, const char* what) {
     return finish(ctx, e, what);
 }
 
-// Shape and size checks of sdu_groupnorm.
+// ---- scratch of the no-allocation GroupNorm (sdu_groupnorm_noalloc)
+// The fp64 per-(image, group) sums and sums of squares of the GroupNorm statistics pass
+// live in this file-scope device array instead of the context's allocated workspace:
+// 64 images x 32 groups x 2 = 32 KiB, held by every device the library runs on until
+// the process ends.  In host code `scratch` is only a symbol: its device address is
+// resolved once per device (hipGetSymbolAddress, with that device current) at sdu_init
+// and every host use goes through that address.
+constexpr int kNoAllocMaxB = 64, kNoAllocMaxG = 32;
+constexpr size_t kNoAllocScratchBytes = (size_t)kNoAllocMaxB * kNoAllocMaxG * 2 * sizeof(double);
+static __device__ __align__(256) double scratch[kNoAllocScratchBytes / sizeof(double)];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kMaxDevices] = {};
+
+// Resolve (once) the address of `scratch` on `device`, which must be current.
+int resolve_scratch(int device) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (device < 0 || device >= kMaxDevices) return SDU_ERR_DEVICE;
+    if (g_scratch_addr[device]) return SDU_OK;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) return SDU_ERR_HIP;
+    g_scratch_addr[device] = p;
+    return SDU_OK;
+}
+
+void* scratch_addr(int device) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    return device >= 0 && device < kMaxDevices ? g_scratch_addr[device] : nullptr;
+}
+
+// Shape and size checks shared by sdu_groupnorm and sdu_groupnorm_noalloc.
 int gn_check(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* x2, const sdu_tensor* gamma,
              const sdu_tensor* beta, const sdu_tensor* y, int B, int HW, int C1, int C2, int groups) {
     const int C = C1 + C2;
@@ -92,6 +124,10 @@ int sdu_init(sdu_ctx** out, const char* weights_dir, uint64_t seed, int flags) {
         hipError_t e = hipGetDevice(&c.device);
         if (e == hipSuccess) e = hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking);
         if (e != hipSuccess) return fail(nullptr, SDU_ERR_DEVICE, std::string("stream: ") + hipGetErrorString(e));
+        if (resolve_scratch(c.device) != SDU_OK) {
+            hipStreamDestroy(c.stream);
+            return fail(nullptr, SDU_ERR_HIP, "cannot resolve the device address of the no-allocation scratch");
+        }
         if (!(flags & SDU_INIT_NO_WEIGHTS)) {
             int st = build_inventory(c);
             if (!st) st = weights_dir ? init_weights_dir(c, weights_dir) : init_weights_seeded(c);
@@ -436,6 +472,26 @@ int sdu_groupnorm(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* x2, const
                              (const f16*)dptr(beta), (f16*)dptr(y), B, HW, groups, eps, silu,
                              (double*)ctx->c.op_ws, ctx->c.stream);
     return finish(ctx, e, "groupnorm");
+}
+
+int sdu_groupnorm_noalloc(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* x2, const sdu_tensor* gamma,
+                          const sdu_tensor* beta, sdu_tensor* y, int B, int HW, int C1, int C2, int groups,
+                          float eps, int silu) {
+    SDU_GUARD(ctx);
+    int st = gn_check(ctx, x, x2, gamma, beta, y, B, HW, C1, C2, groups);
+    if (st) return st;
+    const size_t acc = groupnorm_acc_bytes(B, groups);
+    if (acc > kNoAllocScratchBytes)
+        return fail(ctx, SDU_ERR_ARG, "groupnorm_noalloc: images x groups exceed the 32 KiB scratch (64 x 32)");
+    void* p = scratch_addr(ctx->c.device);
+    if (!p) return fail(ctx, SDU_ERR_HIP, "groupnorm_noalloc: scratch address not resolved for this device");
+    // the statistics pass accumulates into the scratch: clear it with a fill kernel first
+    hipError_t e = zero_launch(p, acc, ctx->c.stream);
+    if (e == hipSuccess)
+        e = groupnorm_launch((const f16*)dptr(x), (const f16*)dptr(x2), C1, C2, (const f16*)dptr(gamma),
+                             (const f16*)dptr(beta), (f16*)dptr(y), B, HW, groups, eps, silu, (double*)p,
+                             ctx->c.stream);
+    return finish(ctx, e, "groupnorm_noalloc");
 }
 
 int sdu_layernorm(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* gamma, const sdu_tensor* beta,

@@ -38,7 +38,7 @@ EXPORTS = [
     "sdu_get_weight", "sdu_param_count", "sdu_forward", "sdu_forward_cfg", "sdu_denoise_lcm",
     "sdu_forward_device", "sdu_denoise_lcm_device", "sdu_denoise_lcm_ex", "sdu_selftest", "sdu_selftest_ex", "sdu_time_proj", "sdu_profile",
     "sdu_tensor_alloc", "sdu_tensor_free", "sdu_tensor_upload", "sdu_tensor_download",
-    "sdu_tensor_device_ptr", "sdu_tensor_bytes", "sdu_groupnorm", "sdu_layernorm", "sdu_matmul",
+    "sdu_tensor_device_ptr", "sdu_tensor_bytes", "sdu_groupnorm", "sdu_groupnorm_noalloc", "sdu_layernorm", "sdu_matmul",
     "sdu_conv2d", "sdu_attention", "sdu_geglu", "sdu_silu", "sdu_add", "sdu_add_bias",
     "sdu_lcm_step",
 ]
@@ -103,6 +103,7 @@ def load(path: str = LIB_PATH):
         "sdu_tensor_device_ptr": ([P], P),
         "sdu_tensor_bytes": ([P], SZ),
         "sdu_groupnorm": ([P, P, P, P, P, P, I, I, I, I, I, F, I], I),
+        "sdu_groupnorm_noalloc": ([P, P, P, P, P, P, I, I, I, I, I, F, I], I),
         "sdu_layernorm": ([P, P, P, P, P, I, I, F], I),
         "sdu_matmul": ([P, P, P, P, P, P, P, I, I, I, I, I], I),
         "sdu_conv2d": ([P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I], I),
