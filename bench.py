@@ -75,7 +75,7 @@ def cpu_baseline(H=64, W=64, timed=3):
 ROOFLINE_IDEAL_MS = {(2, 64): 0.907, (2, 96): 2.18, (16, 64): 6.71}
 
 
-def time_forward(eng, sdu, rng, B, H, W, L, steps, warmup):
+def time_forward(eng, sdu, rng, B, H, W, L, steps, warmup, mark):
     import numpy as np
     lat = rng.standard_normal((B, 4, H, W), np.float32)
     ctx = rng.standard_normal((B, L, 768), np.float32)
@@ -84,14 +84,17 @@ def time_forward(eng, sdu, rng, B, H, W, L, steps, warmup):
 
     def fwd():
         eng.forward_device(d_lat.ptr, d_temb.ptr, d_ctx.ptr, B, H, W, L, d_out.ptr)
+    import torch
     for _ in range(warmup):
         fwd()
     eng.sync()
+    torch.cuda.nvtx.range_push(mark)
     t0 = time.perf_counter()
     for _ in range(steps):
         fwd()
     eng.sync()
     dt = time.perf_counter() - t0
+    torch.cuda.nvtx.range_pop()
     return dt / steps * 1e3, d_out
 
 
@@ -121,6 +124,9 @@ def main():
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device copies of MIB MiB (reference point for the "
                          "FETCH_SIZE / WRITE_SIZE counters) and exit")
+    ap.add_argument("--only", default="", metavar="B,H",
+                    help="only time `steps` forwards at batch B and H x H latents (marked "
+                         "timed_b<B>_<H>x<H>, for profiler runs), print one JSON line and exit")
     args = ap.parse_args()
     if args.copy_probe:
         import torch
@@ -130,7 +136,13 @@ def main():
         for _ in range(5):
             dst.copy_(src)
         torch.cuda.synchronize()
-        print(json.dumps({"copy_probe_bytes": n, "copies": 5}), flush=True)
+        t0 = time.perf_counter()
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / 10
+        print(json.dumps({"copy_probe_bytes": n, "copies": 15, "ms_per_copy": round(dt * 1e3, 4),
+                          "read_plus_write_gbs": round(2 * n / dt / 1e9, 1)}), flush=True)
         return
     if args.gpus != 1:
         print("bench.py: this engine runs on one GPU; multi-GPU runs are not part of this build "
@@ -144,6 +156,19 @@ def main():
     B, H, W, L = 2, 64, 64, 77
     eng = sdu.Engine(seed=1234)
     rng = np.random.default_rng(1)
+    if args.only:
+        b, hw = (int(v) for v in args.only.split(","))
+        ms, _ = time_forward(eng, sdu, rng, b, hw, hw, L, args.steps, args.warmup, f"timed_b{b}_{hw}x{hw}")
+        # one eager pass with each launch timed by its own events (SDU_PROFILE_DUMP=<csv>
+        # makes the library write one line per launch)
+        prof, prof_total = eng.profile(b, hw, hw, L)
+        eng.release()
+        cats = {k: {"calls": v["calls"], "ms": round(v["ms"], 4)} for k, v in
+                sorted(prof.items(), key=lambda kv: -kv[1]["ms"]) if not k.startswith("k:")}
+        print(json.dumps({"only": f"b{b}_{hw}x{hw}", "ms_per_forward": round(ms, 4), "steps": args.steps,
+                          "warmup": args.warmup, "profile_total_ms": round(prof_total, 4),
+                          "categories": cats}), flush=True)
+        return
     lat = rng.standard_normal((B, 4, H, W), np.float32)
     ctx = rng.standard_normal((B, L, 768), np.float32)
     temb = sdu.time_proj(999)
@@ -157,12 +182,16 @@ def main():
         fwd()
     eng.sync()
     torch.cuda.synchronize()
+    # the timed region is marked (roctx range) so that a kernel trace of this command
+    # can select exactly its dispatches
+    torch.cuda.nvtx.range_push("timed_b2_64x64")
     t0 = time.perf_counter()
     for _ in range(args.steps):
         fwd()
     eng.sync()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
+    torch.cuda.nvtx.range_pop()
     ms_step = dt / args.steps * 1e3
     fps = args.steps / dt
     out = d_out.numpy()
@@ -237,7 +266,7 @@ def main():
     # the other single-GPU shapes: B=2 96x96 (9216-token attention) and B=16 64x64
     extra = {}
     for (b, hw, n) in ((2, 96, max(5, args.steps // 4)), (16, 64, max(5, args.steps // 8))):
-        ms, _ = time_forward(eng, sdu, rng, b, hw, hw, L, n, 3)
+        ms, _ = time_forward(eng, sdu, rng, b, hw, hw, L, n, 3, f"timed_b{b}_{hw}x{hw}")
         ideal = ROOFLINE_IDEAL_MS[(b, hw)]
         extra[f"b{b}_{hw}x{hw}"] = {"ms_per_forward": round(ms, 3), "forwards_per_s": round(1e3 / ms, 2),
                                     "images_per_s": round(b * 1e3 / ms, 1), "steps": n,

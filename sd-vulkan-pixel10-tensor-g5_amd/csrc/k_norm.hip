@@ -283,7 +283,7 @@ __device__ __forceinline__ double2 gnf_block_sum2(float v, float u, double2* red
     return t;
 }
 
-// One block per (group, image).  Thread t owns VW consecutive channels (vector
+// One block per (group, image), grid G * B.  Thread t owns VW consecutive channels (vector
 // t % (cpg/VW) of the group) and pixels t / (cpg/VW) + k*P (P = pixels per sweep of the
 // block), k < EP: each load / store is one VW*2-byte vector at a fixed stride, and
 // vectors never straddle the concat split (C1 and C/G are multiples of VW).
@@ -316,7 +316,12 @@ __global__ __launch_bounds__(GNF_THREADS) void gn_fused_kernel(const f16* x, con
     typedef typename GnfVec<VW>::T V;
     __shared__ double2 red[GNF_THREADS / 64];
     const int C = C1 + C2, cpg = C / G, vpg = cpg / VW;
-    const int g = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+    // Workgroups are dealt round-robin over the 8 XCDs, each with its own L2.  The
+    // groups of one image share the 128-byte lines of every pixel row, so each XCD is
+    // given whole images (consecutive groups): a line then crosses the fabric once.
+    const int nblk = gridDim.x;
+    const int q = (nblk & 7) ? (int)blockIdx.x : (int)(blockIdx.x & 7) * (nblk >> 3) + (int)(blockIdx.x >> 3);
+    const int g = q % G, b = q / G, tid = threadIdx.x;
     const int P = GNF_THREADS / vpg;
     const int cv = tid % vpg, pp0 = tid / vpg;
     const bool act = pp0 < P;
@@ -411,7 +416,7 @@ hipError_t groupnorm_launch(const f16* x, const f16* x2, int C1, int C2, const f
         const int ep = nsweep <= 4 ? 4 : nsweep <= 8 ? 8 : nsweep <= 16 ? 16 : 32;
         char name[40];
         snprintf(name, sizeof name, "gn_fused_kernel<%d,%d>", ep, vw);
-        const dim3 grid(G, B);
+        const dim3 grid(G * B);
         launch_timed(name, 0.0, 2.0 * xbytes, [&] {
 #define GNF_LAUNCH(EPV, VWV)                                                                                 \
     SDU_LAUNCH((gn_fused_kernel<EPV, VWV>), grid, dim3(GNF_THREADS), 0, s, x, x2, C1, C2, gamma, beta, y, \
