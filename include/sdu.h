@@ -127,6 +127,34 @@ int sdu_denoise_lcm_ex(sdu_ctx* ctx, const float* d_lat, const float* d_cond,
                        const float* d_uncond, int H, int W, int L, int steps, float guidance,
                        int cfg_steps, const float* d_noise, uint64_t noise_seed, float* d_out);
 
+/* Latent decoder: replaces vaeDecode (VulkanUnetPipeline.kt:55-61), the LiteRT export of
+ * diffusers AutoencoderTiny("madebyollin/taesd").decode (tools/export_taesd.py:52-54, contract
+ * at :2).  sdu_taesd_init creates the decoder's weights: from weights_dir (one raw fp16 file
+ * per diffusers key, decoder.layers.<i>..., as the UNet's weight directory) or, when
+ * weights_dir is NULL, seeded (conv weights N(0, 0.04); biases 0, or N(0, .02) with
+ * SDU_INIT_RANDOM_AFFINE).  Decode: fp32 latent [B,4,H,W] -> fp32 image [B,3,8H,8W] in
+ * about [-1, 1] (B 1..16, H and W 8..128), one captured graph per shape. */
+int sdu_taesd_init(sdu_ctx* ctx, const char* weights_dir, uint64_t seed, int flags);
+int sdu_taesd_decode(sdu_ctx* ctx, const float* lat, int B, int H, int W, float* img);
+int sdu_taesd_decode_device(sdu_ctx* ctx, const float* d_lat, int B, int H, int W, float* d_img);
+
+/* Text encoder: replaces clipContext (VulkanUnetPipeline.kt:48-53), the LiteRT export of SD1.5's
+ * CLIP text encoder (CLIPTextModel): int32 token ids [B,77] -> fp32 last hidden state
+ * [B,77,768], the UNet's context (B 1..64).  Weights from weights_dir (text_model.* keys,
+ * Linear [in, out]) or seeded (Linear and embeddings N(0, 0.02); LayerNorm gamma 1, beta 0,
+ * biases 0, or the affine mode). */
+int sdu_clip_init(sdu_ctx* ctx, const char* weights_dir, uint64_t seed, int flags);
+int sdu_clip_encode(sdu_ctx* ctx, const int32_t* ids, int B, float* out);
+int sdu_clip_encode_device(sdu_ctx* ctx, const int32_t* d_ids, int B, float* d_out);
+
+/* End-to-end image: VulkanUnetPipeline.generate (VulkanUnetPipeline.kt:63-97).  CLIP of the
+ * prompt and empty-prompt ids in one batch, an initial latent N(0, 1) drawn on the device from
+ * `seed`, the LCM denoise of sdu_denoise_lcm_ex (steps, guidance, cfg_steps, noise from
+ * `seed`), then the TAESD decoder.  image: fp32 [3, 8H, 8W] in about [-1, 1] (toBitmap,
+ * :99-109, maps (x + 1) * 127.5).  Needs sdu_clip_init and sdu_taesd_init. */
+int sdu_generate(sdu_ctx* ctx, const int32_t* cond_ids, const int32_t* uncond_ids, int H, int W,
+                 int steps, float guidance, int cfg_steps, uint64_t seed, float* image);
+
 /* unetSelfTest (vk_engine.cpp:811-851): reads fixture_dir/IN_lat.bin (fp16 [4,64,64]),
  * IN_ctx.bin (fp16 [77,768]), IN_temb_proj.bin (fp16 [320]) and OUT_y.bin (fp16),
  * runs B=1 and B=2 (same input in both slots) and returns the largest
@@ -203,6 +231,8 @@ int sdu_layernorm(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* gamma, co
 /* Epilogue flags for sdu_matmul / sdu_conv2d */
 #define SDU_EPI_GEGLU   0x1 /* w rows interleaved per 32 (a,b); y[:, N/2] = a * gelu_erf(b)   */
 #define SDU_EPI_OUT_F32 0x2 /* y is float32                                                    */
+#define SDU_EPI_RELU    0x4 /* y = max(y, 0) after bias and residual (TAESD decoder convs)     */
+#define SDU_EPI_QUICK_GELU 0x8 /* y = y * sigmoid(1.702 y) after bias (CLIP text encoder fc1)   */
 
 /* matmul (vk_engine.cpp:612-613) with fused epilogue:
  * y[M,N] = a[M,K] . w[N,K]^T (+ bias[N]) (+ residual[M,N]).
@@ -227,6 +257,12 @@ int sdu_conv2d(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* w, const sdu
 int sdu_attention(sdu_ctx* ctx, const sdu_tensor* q, const sdu_tensor* k, const sdu_tensor* v,
                   sdu_tensor* o, int B, int heads, int Sq, int Sk, int d, int ldq, int ldk,
                   int ldv, int ldo, float scale);
+/* sdu_attention with flags: SDU_ATTN_CAUSAL masks key j > query i (Sq == Sk), the causal
+ * self-attention of the CLIP text encoder behind VulkanUnetPipeline.kt:48-53. */
+#define SDU_ATTN_CAUSAL 0x1
+int sdu_attention_ex(sdu_ctx* ctx, const sdu_tensor* q, const sdu_tensor* k, const sdu_tensor* v,
+                     sdu_tensor* o, int B, int heads, int Sq, int Sk, int d, int ldq, int ldk,
+                     int ldv, int ldo, float scale, int flags);
 
 /* GEGLU (geglu_f32.comp): y[t,c] = g[t,c] * gelu_erf(g[t,C2+c]). */
 int sdu_geglu(sdu_ctx* ctx, const sdu_tensor* g, sdu_tensor* y, int T, int C2);

@@ -49,6 +49,13 @@ int finish(sdu_ctx* ctx, hipError_t e, const char* what) {
     return SDU_OK;
 }
 
+// Output activation of an op-level GEMM / conv from its epilogue flags (-1: both set).
+int epi_act(int flags) {
+    const bool relu = (flags & SDU_EPI_RELU) != 0, qg = (flags & SDU_EPI_QUICK_GELU) != 0;
+    if (relu && qg) return -1;
+    return relu ? ACT_RELU : qg ? ACT_QUICK_GELU : ACT_NONE;
+}
+
 // An op-level GEMM on the context's scratch.  Other ops reuse that scratch, so the
 // split-K tile counters at its head are cleared before a split launch.
 int op_gemm(sdu_ctx* ctx, const GemmArgs& g, const char* what) {
@@ -148,6 +155,8 @@ int sdu_release(sdu_ctx* ctx) {
     Ctx& c = ctx->c;
     hipStreamSynchronize(c.stream);
     free_fwd_states(c);
+    aux_free(c.taesd);
+    aux_free(c.clip);
     if (c.wpool) hipFree(c.wpool);
     if (c.op_ws) hipFree(c.op_ws);
     hipStreamDestroy(c.stream);
@@ -269,6 +278,114 @@ int sdu_denoise_lcm_ex(sdu_ctx* ctx, const float* d_lat, const float* d_cond, co
     return guarded(ctx, [&] {
         return unet_denoise_device(ctx->c, d_lat, d_cond, d_uncond, H, W, L, steps, guidance, cfg_steps, d_noise,
                                    noise_seed, d_out);
+    });
+}
+
+// ---- TAESD decoder and CLIP text encoder (VulkanUnetPipeline.kt:48-61)
+
+int sdu_taesd_init(sdu_ctx* ctx, const char* weights_dir, uint64_t seed, int flags) {
+    SDU_GUARD(ctx);
+    if (flags & ~SDU_INIT_RANDOM_AFFINE) return fail(ctx, SDU_ERR_ARG, "bad flags");
+    return guarded(ctx, [&] { return taesd_create(ctx->c, weights_dir, seed, flags); });
+}
+
+int sdu_taesd_decode_device(sdu_ctx* ctx, const float* d_lat, int B, int H, int W, float* d_img) {
+    SDU_GUARD(ctx);
+    if (!d_lat || !d_img) return fail(ctx, SDU_ERR_ARG, "null argument");
+    return guarded(ctx, [&] { return taesd_decode_device(ctx->c, d_lat, B, H, W, d_img); });
+}
+
+int sdu_taesd_decode(sdu_ctx* ctx, const float* lat, int B, int H, int W, float* img) {
+    SDU_GUARD(ctx);
+    if (!lat || !img) return fail(ctx, SDU_ERR_ARG, "null argument");
+    if (B < 1 || B > 16 || H < 8 || W < 8 || H > 128 || W > 128)
+        return fail(ctx, SDU_ERR_ARG, "TAESD decode: B in 1..16, H and W in 8..128");
+    return guarded(ctx, [&]() -> int {
+        const size_t ni = (size_t)B * 4 * H * W, no = (size_t)B * 3 * 64 * H * W;
+        float* d = nullptr;
+        hipError_t e = hipMalloc(&d, (ni + no) * 4);
+        if (e != hipSuccess) return fail(ctx, SDU_ERR_OOM, "staging allocation failed");
+        hipStream_t s = ctx->c.stream;
+        int st = SDU_OK;
+        if ((e = hipMemcpyAsync(d, lat, ni * 4, hipMemcpyHostToDevice, s))) st = hipfail(ctx, e, "upload");
+        if (!st) st = taesd_decode_device(ctx->c, d, B, H, W, d + ni);
+        if (!st && ((e = hipMemcpyAsync(img, d + ni, no * 4, hipMemcpyDeviceToHost, s)) || (e = hipStreamSynchronize(s))))
+            st = hipfail(ctx, e, "download");
+        hipStreamSynchronize(s);
+        hipFree(d);
+        return st;
+    });
+}
+
+int sdu_clip_init(sdu_ctx* ctx, const char* weights_dir, uint64_t seed, int flags) {
+    SDU_GUARD(ctx);
+    if (flags & ~SDU_INIT_RANDOM_AFFINE) return fail(ctx, SDU_ERR_ARG, "bad flags");
+    return guarded(ctx, [&] { return clip_create(ctx->c, weights_dir, seed, flags); });
+}
+
+int sdu_clip_encode_device(sdu_ctx* ctx, const int32_t* d_ids, int B, float* d_out) {
+    SDU_GUARD(ctx);
+    if (!d_ids || !d_out) return fail(ctx, SDU_ERR_ARG, "null argument");
+    return guarded(ctx, [&] { return clip_encode_device(ctx->c, d_ids, B, d_out); });
+}
+
+int sdu_clip_encode(sdu_ctx* ctx, const int32_t* ids, int B, float* out) {
+    SDU_GUARD(ctx);
+    if (!ids || !out) return fail(ctx, SDU_ERR_ARG, "null argument");
+    if (B < 1 || B > 64) return fail(ctx, SDU_ERR_ARG, "CLIP encode: B in 1..64");
+    return guarded(ctx, [&]() -> int {
+        const size_t ni = (size_t)B * 77, no = (size_t)B * 77 * 768;
+        char* d = nullptr;
+        hipError_t e = hipMalloc(&d, ni * 4 + no * 4);
+        if (e != hipSuccess) return fail(ctx, SDU_ERR_OOM, "staging allocation failed");
+        hipStream_t s = ctx->c.stream;
+        int st = SDU_OK;
+        if ((e = hipMemcpyAsync(d, ids, ni * 4, hipMemcpyHostToDevice, s))) st = hipfail(ctx, e, "upload");
+        if (!st) st = clip_encode_device(ctx->c, (const int32_t*)d, B, (float*)(d + ni * 4));
+        if (!st && ((e = hipMemcpyAsync(out, d + ni * 4, no * 4, hipMemcpyDeviceToHost, s)) ||
+                    (e = hipStreamSynchronize(s))))
+            st = hipfail(ctx, e, "download");
+        hipStreamSynchronize(s);
+        hipFree(d);
+        return st;
+    });
+}
+
+int sdu_generate(sdu_ctx* ctx, const int32_t* cond_ids, const int32_t* uncond_ids, int H, int W, int steps,
+                 float guidance, int cfg_steps, uint64_t seed, float* image) {
+    SDU_GUARD(ctx);
+    if (!cond_ids || !uncond_ids || !image) return fail(ctx, SDU_ERR_ARG, "null argument");
+    if (!ctx->c.clip || !ctx->c.taesd) return fail(ctx, SDU_ERR_WEIGHT, "sdu_generate needs sdu_clip_init and sdu_taesd_init");
+    if (H < 8 || W < 8 || H > 128 || W > 128 || H % 8 || W % 8) return fail(ctx, SDU_ERR_ARG, "H, W: multiples of 8 in 8..128");
+    return guarded(ctx, [&]() -> int {
+        const size_t L = 77, C = 768, nl = (size_t)4 * H * W, ni = (size_t)3 * 64 * H * W;
+        char* d = nullptr;
+        const size_t bytes = 2 * L * 4 + 2 * L * C * 4 + 2 * nl * 4 + ni * 4;
+        hipError_t e = hipMalloc(&d, bytes);
+        if (e != hipSuccess) return fail(ctx, SDU_ERR_OOM, "staging allocation failed");
+        int32_t* d_ids = (int32_t*)d;
+        float* d_ctx = (float*)(d + 2 * L * 4);
+        float* d_lat = d_ctx + 2 * L * C;
+        float* d_x = d_lat + nl;
+        float* d_img = d_x + nl;
+        hipStream_t s = ctx->c.stream;
+        Ctx& c = ctx->c;
+        int st = SDU_OK;
+        // prompt and empty-prompt contexts in one CLIP batch (VulkanUnetPipeline.kt:66-72);
+        // initial latent N(0, 1) * initialScale (= 1, LcmScheduler.kt:20) drawn on the device
+        if ((e = hipMemcpyAsync(d_ids, cond_ids, L * 4, hipMemcpyHostToDevice, s)) ||
+            (e = hipMemcpyAsync(d_ids + L, uncond_ids, L * 4, hipMemcpyHostToDevice, s)) ||
+            (e = gen_normal_f32_launch(d_lat, (int64_t)nl, fnv1a64("lcm.latent") ^ splitmix64(seed), s)))
+            st = hipfail(ctx, e, "generate");
+        if (!st) st = clip_encode_device(c, d_ids, 2, d_ctx);
+        if (!st) st = unet_denoise_device(c, d_lat, d_ctx, d_ctx + L * C, H, W, (int)L, steps, guidance, cfg_steps,
+                                          nullptr, seed, d_x);
+        if (!st) st = taesd_decode_device(c, d_x, 1, H, W, d_img);
+        if (!st && ((e = hipMemcpyAsync(image, d_img, ni * 4, hipMemcpyDeviceToHost, s)) || (e = hipStreamSynchronize(s))))
+            st = hipfail(ctx, e, "download");
+        hipStreamSynchronize(s);
+        hipFree(d);
+        return st;
     });
 }
 
@@ -514,7 +631,7 @@ int sdu_matmul(sdu_ctx* ctx, const sdu_tensor* a, const sdu_tensor* a2, const sd
     const int f32 = (flags & SDU_EPI_OUT_F32) != 0;
     const int K1 = K - K2;
     if (M < 1 || N < 1 || K < 8 || K % 8 || K2 < 0 || K2 > K || K1 % 8 || (K2 && !a2) ||
-        (geglu && N % 64))
+        (geglu && N % 64) || epi_act(flags) < 0)
         return fail(ctx, SDU_ERR_ARG, "bad matmul shape");
     const int Nout = geglu ? N / 2 : N;
     if (!fits(a, (size_t)M * K1 * 2) || (K2 && !fits(a2, (size_t)M * K2 * 2)) || !fits(w, (size_t)N * K * 2) ||
@@ -532,6 +649,7 @@ int sdu_matmul(sdu_ctx* ctx, const sdu_tensor* a, const sdu_tensor* a2, const sd
     g.C = dptr(y); g.ldc = Nout;
     g.out_mode = f32 ? OUT_F32 : OUT_F16;
     g.geglu = geglu;
+    g.act = epi_act(flags);
     return op_gemm(ctx, g, "matmul");
 }
 
@@ -542,7 +660,7 @@ int sdu_conv2d(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* w, const sdu
     const int f32 = (flags & SDU_EPI_OUT_F32) != 0;
     if (B < 1 || H < 1 || W < 1 || Ci < 8 || Ci % 8 || Co < 1 || (ksize != 1 && ksize != 3) ||
         (stride != 1 && stride != 2) || (upsample && stride != 1) || (ksize == 1 && (stride != 1 || upsample)) ||
-        (flags & SDU_EPI_GEGLU))
+        (flags & SDU_EPI_GEGLU) || epi_act(flags) < 0)
         return fail(ctx, SDU_ERR_ARG, "bad conv2d shape");
     const int Ho = upsample ? 2 * H : (stride == 2 ? (H - 1) / 2 + 1 : H);
     const int Wo = upsample ? 2 * W : (stride == 2 ? (W - 1) / 2 + 1 : W);
@@ -571,13 +689,22 @@ int sdu_conv2d(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* w, const sdu
     g.res = (const f16*)dptr(residual); g.ldr = Co;
     g.C = dptr(y); g.ldc = Co;
     g.out_mode = f32 ? OUT_F32 : OUT_F16;
+    g.act = epi_act(flags);
     return op_gemm(ctx, g, "conv2d");
 }
 
 int sdu_attention(sdu_ctx* ctx, const sdu_tensor* q, const sdu_tensor* k, const sdu_tensor* v,
                   sdu_tensor* o, int B, int heads, int Sq, int Sk, int d, int ldq, int ldk, int ldv,
                   int ldo, float scale) {
+    return sdu_attention_ex(ctx, q, k, v, o, B, heads, Sq, Sk, d, ldq, ldk, ldv, ldo, scale, 0);
+}
+
+int sdu_attention_ex(sdu_ctx* ctx, const sdu_tensor* q, const sdu_tensor* k, const sdu_tensor* v,
+                     sdu_tensor* o, int B, int heads, int Sq, int Sk, int d, int ldq, int ldk, int ldv,
+                     int ldo, float scale, int flags) {
     SDU_GUARD(ctx);
+    const int causal = (flags & SDU_ATTN_CAUSAL) != 0;
+    if ((flags & ~SDU_ATTN_CAUSAL) || (causal && Sq != Sk)) return fail(ctx, SDU_ERR_ARG, "bad attention flags");
     if (B < 1 || heads < 1 || Sq < 1 || Sk < 1 || d < 8 || d > 160 || d % 8 || ldq < heads * d ||
         ldk < heads * d || ldv < heads * d || ldo < heads * d || ldq % 8 || ldk % 8 || ldv % 8 || ldo % 8 ||
         B > 65535 || heads > 65535)
@@ -586,7 +713,7 @@ int sdu_attention(sdu_ctx* ctx, const sdu_tensor* q, const sdu_tensor* k, const 
         !fits(v, (size_t)B * Sk * ldv * 2) || !fits(o, (size_t)B * Sq * ldo * 2))
         return fail(ctx, SDU_ERR_ARG, "attention tensor too small");
     AttnArgs a{(const f16*)dptr(q), (const f16*)dptr(k), (const f16*)dptr(v), (f16*)dptr(o), B, heads, Sq, Sk,
-               d, ldq, ldk, ldv, ldo, scale};
+               d, ldq, ldk, ldv, ldo, scale, causal};
     return finish(ctx, attention_launch(a, ctx->c.stream), "attention");
 }
 

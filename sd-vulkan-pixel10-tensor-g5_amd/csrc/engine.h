@@ -12,7 +12,7 @@
 
 namespace sdu {
 
-enum WKind { WK_CONV = 0, WK_LINEAR = 1, WK_NORM_W = 2, WK_NORM_B = 3, WK_BIAS = 4 };
+enum WKind { WK_CONV = 0, WK_LINEAR = 1, WK_NORM_W = 2, WK_NORM_B = 3, WK_BIAS = 4, WK_EMBED = 5 };
 
 // One named UNet parameter.  `dev` points into the weight pool; the device layout
 // is described by (layout, ci_pad): conv weights are [Co, kh, kw, Ci_pad] (the
@@ -82,6 +82,35 @@ struct ProfAcc {
 };
 
 struct FwdState;  // per-shape graph state (unet.cpp)
+struct AuxState;  // per-shape graph state of an auxiliary network (taesd.cpp, clip.cpp)
+
+// The weights and planned graphs of an auxiliary network: the TAESD latent decoder or
+// the CLIP text encoder.  Its own fp16 pool, in the device layouts its kernels read,
+// registered and loaded like the UNet's (same seeded generator, same weight-file format).
+struct AuxNet {
+    int kind = 0;  // AUX_TAESD | AUX_CLIP
+    f16* pool = nullptr;
+    size_t pool_bytes = 0;
+    std::vector<WeightRec> weights;
+    std::unordered_map<std::string, int> widx;
+    std::vector<char> contig;  // placed right after the previous tensor (fused q/k/v blocks)
+    std::vector<AuxState*> states;  // owned, LRU-capped
+    uint64_t use_clock = 0;
+    // TAESD: conv_out with the output affine y = 2 x - 1 folded in (2 W fp16, 2 b - 1 fp32)
+    f16* w_out2 = nullptr;
+    float* b_out2 = nullptr;
+    int add(const std::string& name, std::vector<int64_t> shape, int kind, int layout = GL_PLAIN, int ci_pad = 0,
+            bool follows = false);
+    const WeightRec* w(const std::string& name) const {
+        auto it = widx.find(name);
+        return it == widx.end() ? nullptr : &weights[it->second];
+    }
+    f16* wd(const std::string& name) const {
+        const WeightRec* r = w(name);
+        return r ? r->dev : nullptr;
+    }
+};
+enum AuxKind { AUX_TAESD = 1, AUX_CLIP = 2 };
 
 struct Ctx {
     int device = 0;
@@ -110,6 +139,10 @@ struct Ctx {
     uint64_t use_clock = 0;
     float* op_ws = nullptr;     // scratch for op-level calls
     size_t op_ws_bytes = 0;
+
+    // auxiliary networks (created on demand by sdu_taesd_init / sdu_clip_init)
+    AuxNet* taesd = nullptr;
+    AuxNet* clip = nullptr;
 
     // profiling
     bool profiling = false;
@@ -141,8 +174,22 @@ int set_weight_canonical(Ctx& c, const WeightRec& r, const float* data);
 // the loaded ones (all blocks, or the one whose prefix `name` starts with); synchronous.
 int fold_weights(Ctx& c, const std::string& name = std::string());
 int get_weight_canonical(Ctx& c, const WeightRec& r, float* out);
+// One tensor: seeded values (conv / linear / embedding N(0, wstd); norms and biases per the
+// init mode), or read from <dir>/<name>.bin (raw fp16, Linear stored [in, out]).
+int gen_weight(Ctx& c, const WeightRec& r, uint64_t seed, bool affine, double wstd);
+int load_weight_file(Ctx& c, const WeightRec& r, const std::string& dir);
+// Allocate an auxiliary network's pool for its registered tensors and place them.
+int aux_alloc(Ctx& c, AuxNet& n, size_t extra_bytes);
+void aux_free(AuxNet* n);
 int ensure_op_ws(Ctx& c, size_t bytes);
 int set_err(Ctx* c, int code, const std::string& msg);
+
+// taesd.cpp: latent [B, 4, H, W] fp32 -> image [B, 3, 8H, 8W] fp32 in about [-1, 1]
+int taesd_create(Ctx& c, const char* weights_dir, uint64_t seed, int flags);
+int taesd_decode_device(Ctx& c, const float* d_lat, int B, int H, int W, float* d_img);
+// clip.cpp: token ids [B, 77] -> last hidden state [B, 77, 768] fp32
+int clip_create(Ctx& c, const char* weights_dir, uint64_t seed, int flags);
+int clip_encode_device(Ctx& c, const int32_t* d_ids, int B, float* d_out);
 
 // unet.cpp
 int unet_forward_host(Ctx& c, const float* lat, const float* temb, const float* ctx, int B, int H,

@@ -46,8 +46,9 @@ __device__ __forceinline__ int key_perm(int r) {
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Online-softmax update for NSUB 32-key sub-tiles of raw scores s (S^T layout)
-// followed by O^T += V^T . P^T.  `kvalid` = number of valid keys in the tile
-// (< NSUB*32 only on the last tile).  vt: V^T tile [dim][key] with row stride vstr.
+// followed by O^T += V^T . P^T.  `kvalid` = number of valid keys in the tile for this
+// lane's query (< NSUB*32 only on the last tile, or below the causal limit; may be <= 0).
+// vt: V^T tile [dim][key] with row stride vstr.
 template <int NSUB, int MTD, bool LSUM>
 __device__ __forceinline__ void softmax_pv(floatx16 (&s)[NSUB], int kvalid, float c, float& m_run,
                                            float& l_run, floatx16 (&o)[MTD], const f16* vt, int vstr,
@@ -76,7 +77,9 @@ __device__ __forceinline__ void softmax_pv(floatx16 (&s)[NSUB], int kvalid, floa
         l_run *= alpha;
         m_run = m_new;
     }
-    const float nm = -m_run;
+    // (a lane whose keys so far were all masked keeps m_run = -inf: subtract 0, so that
+    // its masked scores give exp2(-inf) = 0 rather than exp2(-inf + inf))
+    const float nm = m_run == -INFINITY ? 0.f : -m_run;
     float psum = 0.f;
 #pragma unroll
     for (int sub = 0; sub < NSUB; ++sub)
@@ -414,7 +417,9 @@ __global__ __launch_bounds__(NSPLIT * 64) void attn_split_kernel(AttnArgs a) {
         __builtin_amdgcn_s_setprio(2);
         if (it + NSPLIT < ntile) load(kb + NSPLIT * KTS);
         __builtin_amdgcn_s_setprio(1);
-        softmax_pv<1, MTD, LSUM>(s, min(KTS, a.Sk - kb), c, m_run, l_run, o, vt, VSTRS, hl, lrow, lk);
+        // causal: query q0 + lrow sees keys up to itself
+        const int kv = a.causal ? min(KTS, min(a.Sk, q0 + lrow + 1) - kb) : min(KTS, a.Sk - kb);
+        softmax_pv<1, MTD, LSUM>(s, kv, c, m_run, l_run, o, vt, VSTRS, hl, lrow, lk);
         __builtin_amdgcn_s_setprio(0);
         __builtin_amdgcn_wave_barrier();
     }
@@ -479,7 +484,7 @@ static void launch_cfg(const AttnArgs& a, hipStream_t s) {
     // leave < 512 blocks.  Fewer query waves (e.g. 1024 queries x 16 heads), and short
     // key sequences (cross-attention over the 77 context tokens), go to the key-split
     // kernel: its extra waves, or not staging a few K/V tiles per block, win.
-    if (qwaves >= 1024 && a.Sk > 128) {
+    if (qwaves >= 1024 && a.Sk > 128 && !a.causal) {
         const int nw = ((a.Sq + 127) / 128) * bh >= 512 ? 4 : 2;
         snprintf(name, sizeof name, "attn_kernel<%d,%d,%d,%d>", KS, MTD, nw, (int)LSUM);
         const dim3 grid((a.Sq + nw * 32 - 1) / (nw * 32), a.heads, a.B);
@@ -514,7 +519,8 @@ static void launch_d(const AttnArgs& a, hipStream_t s) {
 }
 
 hipError_t attention_launch(const AttnArgs& a, hipStream_t s) {
-    if (a.d <= 0 || a.d > 160 || (a.d & 7) || a.Sq <= 0 || a.Sk <= 0 || !(a.scale > 0.f))
+    if (a.d <= 0 || a.d > 160 || (a.d & 7) || a.Sq <= 0 || a.Sk <= 0 || !(a.scale > 0.f) ||
+        (a.causal && a.Sq != a.Sk))
         return hipErrorInvalidValue;
     const int d = a.d;
     if (d <= 32) launch_d<2, 1>(a, s);

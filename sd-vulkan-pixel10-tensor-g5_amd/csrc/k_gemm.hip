@@ -12,7 +12,7 @@
 //     1x1 shortcut (:634) summed into its conv2.
 // Epilogue (fused; the reference runs these as separate AB/AB2/ADD/GEGLU passes):
 // + bias[n] + bias2[n] (fp32 time projection), GEGLU over interleaved a/b column
-// blocks, + residual, store fp16 / fp32 / fp32-NCHW.  A LayerNorm (layernorm_f32.comp,
+// blocks, + residual, activation (ReLU / quick-GELU), store fp16 / fp32 / fp32-NCHW.  A LayerNorm (layernorm_f32.comp,
 // vk_engine.cpp:652, :658, :666) between two GEMMs runs inside them: the producer adds
 // each output row's sum and sum of squares into a row-statistics buffer, and the
 // consumer, reading the un-normalised rows as A, applies rstd * (acc - mean * colsum(W))
@@ -43,6 +43,7 @@ __device__ __forceinline__ void epi_store(const GemmArgs& a, int m, int n, float
         v = v * gelu_erf(gate);
     }
     if (a.res) v += (float)a.res[(int64_t)m * a.ldr + nout];
+    v = apply_act(a.act, v);
     if (a.out_mode == OUT_F16) {
         ((f16*)a.C)[(int64_t)m * a.ldc + nout] = (f16)v;
     } else if (a.out_mode == OUT_F32) {
@@ -190,7 +191,7 @@ __device__ __forceinline__ void reduce_rows(const GemmArgs& a, const int (&m)[R]
             float x = v[r][e];
             if (geglu) x *= gelu_erf(g[r][e]);
             if (a.res) x += (float)rh[e];
-            o[e] = x;
+            o[e] = apply_act(a.act, x);
         }
         ov[r] = make_uint4(0, 0, 0, 0);
         if (!(valid >> r & 1)) continue;
@@ -790,6 +791,10 @@ void gemm_kernel(GemmArgs a) {
                 const f16* rh = (const f16*)&rres[ip][k];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) v[e] += (float)rh[e];
+            }
+            if (a.act) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = apply_act(a.act, v[e]);
             }
             if (a.out_mode == OUT_F16) {
                 uint4 o;

@@ -15,7 +15,7 @@
 namespace sdu {
 
 __global__ void nchw_to_nhwc_kernel(const float* src, f16* dst, int B, int Bsrc, int C, int Cpad,
-                                    int HW) {
+                                    int HW, int tanh_clamp) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t total = (int64_t)B * HW * Cpad;
     if (i >= total) return;
@@ -24,15 +24,48 @@ __global__ void nchw_to_nhwc_kernel(const float* src, f16* dst, int B, int Bsrc,
     const int b = (int)(pix / HW), p = (int)(pix % HW);
     float v = 0.f;
     if (c < C) v = src[((int64_t)(b % Bsrc) * C + c) * HW + p];
+    if (tanh_clamp) v = 3.0f * tanhf(v * (1.0f / 3.0f));
     dst[i] = (f16)v;
 }
 
 hipError_t nchw_to_nhwc_launch(const float* src, f16* dst, int B, int Bsrc, int C, int Cpad, int HW,
-                               hipStream_t s) {
+                               hipStream_t s, int tanh_clamp) {
     const int64_t total = (int64_t)B * HW * Cpad;
     launch_timed("nchw_to_nhwc_kernel", 0.0, 4.0 * Bsrc * C * HW + 2.0 * total, [&] {
         SDU_LAUNCH(nchw_to_nhwc_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
-                           src, dst, B, Bsrc, C, Cpad, HW);
+                           src, dst, B, Bsrc, C, Cpad, HW, tanh_clamp);
+    });
+    return hipGetLastError();
+}
+
+// One thread per 8 channels of one token.
+__global__ void embed_kernel(const int32_t* ids, const f16* tok, const f16* pos, f16* out, int B, int S, int C,
+                             int vocab) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int cpr = C / 8;
+    if (i >= (int64_t)B * S * cpr) return;
+    const int64_t row = i / cpr;
+    const int c8 = (int)(i - row * cpr) * 8;
+    const int t = (int)(row % S);
+    const int id = min(max(ids[row], 0), vocab - 1);
+    const uint4 a = *(const uint4*)(tok + (int64_t)id * C + c8);
+    const uint4 p = *(const uint4*)(pos + (int64_t)t * C + c8);
+    const f16* ah = (const f16*)&a;
+    const f16* ph = (const f16*)&p;
+    uint4 o;
+    f16* oh = (f16*)&o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) oh[e] = (f16)((float)ah[e] + (float)ph[e]);
+    *(uint4*)(out + row * C + c8) = o;
+}
+
+hipError_t embed_launch(const int32_t* ids, const f16* tok, const f16* pos, f16* out, int B, int S, int C,
+                        int vocab, hipStream_t s) {
+    if (B < 1 || S < 1 || C % 8 || vocab < 1) return hipErrorInvalidValue;
+    const int64_t total = (int64_t)B * S * (C / 8);
+    launch_timed("embed_kernel", 0.0, 4.0 * B * S * C + 4.0 * B * S, [&] {
+        SDU_LAUNCH(embed_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, ids, tok, pos, out, B, S, C,
+                   vocab);
     });
     return hipGetLastError();
 }

@@ -17,6 +17,7 @@
 
 #include <cstdio>
 #include <cstring>
+#include <algorithm>
 #include <fstream>
 
 namespace sdu {
@@ -312,26 +313,31 @@ static int64_t dev_to_canon_index(const WeightRec& r, int64_t i) {
     return i;
 }
 
+int gen_weight(Ctx& c, const WeightRec& r, uint64_t seed, bool affine, double wstd) {
+    GenDesc g{};
+    g.key = fnv1a64(r.name.c_str()) ^ splitmix64(seed);
+    g.n = r.dev_n;
+    g.layout = r.layout;
+    if (r.layout == GL_CONV_OHWI) {
+        g.co = (int)r.shape[0]; g.ci = (int)r.shape[1]; g.kh = (int)r.shape[2];
+        g.kw = (int)r.shape[3]; g.ci_pad = r.ci_pad;
+    } else if (r.layout == GL_GEGLU_PERM) {
+        g.half_rows = (int)(r.shape[0] / 2);
+        g.cols = r.shape.size() > 1 ? (int)r.shape[1] : 1;
+    }
+    if (r.kind == WK_CONV || r.kind == WK_LINEAR || r.kind == WK_EMBED) { g.mean = 0.0; g.stdv = wstd; }
+    else if (!affine) { g.constant = 1; g.mean = (r.kind == WK_NORM_W) ? 1.0 : 0.0; }
+    else { g.mean = (r.kind == WK_NORM_W) ? 1.0 : 0.0; g.stdv = 0.02; }
+    hipError_t e = gen_launch(r.dev, g, c.stream);
+    if (e != hipSuccess) return set_err(&c, SDU_ERR_HIP, std::string("weight generator: ") + hipGetErrorString(e));
+    return SDU_OK;
+}
+
 int init_weights_seeded(Ctx& c) {
     const bool affine = (c.flags & SDU_INIT_RANDOM_AFFINE) != 0;
-    const uint64_t sm = splitmix64(c.seed);
     for (const WeightRec& r : c.weights) {
-        GenDesc g{};
-        g.key = fnv1a64(r.name.c_str()) ^ sm;
-        g.n = r.dev_n;
-        g.layout = r.layout;
-        if (r.layout == GL_CONV_OHWI) {
-            g.co = (int)r.shape[0]; g.ci = (int)r.shape[1]; g.kh = (int)r.shape[2];
-            g.kw = (int)r.shape[3]; g.ci_pad = r.ci_pad;
-        } else if (r.layout == GL_GEGLU_PERM) {
-            g.half_rows = (int)(r.shape[0] / 2);
-            g.cols = r.shape.size() > 1 ? (int)r.shape[1] : 1;
-        }
-        if (r.kind == WK_CONV || r.kind == WK_LINEAR) { g.mean = 0.0; g.stdv = 0.02; }
-        else if (!affine) { g.constant = 1; g.mean = (r.kind == WK_NORM_W) ? 1.0 : 0.0; }
-        else { g.mean = (r.kind == WK_NORM_W) ? 1.0 : 0.0; g.stdv = 0.02; }
-        hipError_t e = gen_launch(r.dev, g, c.stream);
-        if (e != hipSuccess) return set_err(&c, SDU_ERR_HIP, std::string("weight generator: ") + hipGetErrorString(e));
+        int st = gen_weight(c, r, c.seed, affine, 0.02);
+        if (st) return st;
     }
     return fold_weights(c);
 }
@@ -348,34 +354,71 @@ static int upload_canonical_f16(Ctx& c, const WeightRec& r, const uint16_t* cano
     return SDU_OK;
 }
 
+int load_weight_file(Ctx& c, const WeightRec& r, const std::string& dir) {
+    const std::string path = dir + "/" + r.name + ".bin";
+    std::ifstream f(path, std::ios::binary | std::ios::ate);
+    if (!f) return set_err(&c, SDU_ERR_WEIGHT, "weight missing: " + path);
+    const int64_t sz = (int64_t)f.tellg();
+    const int64_t n = r.numel();
+    if (sz != n * 2)
+        return set_err(&c, SDU_ERR_WEIGHT, "weight size mismatch: " + path + " has " + std::to_string(sz) +
+                                               " bytes, expected " + std::to_string(n * 2));
+    std::vector<uint16_t> raw((size_t)n);
+    f.seekg(0);
+    if (!f.read((char*)raw.data(), n * 2)) return set_err(&c, SDU_ERR_IO, "read failed: " + path);
+    std::vector<uint16_t> canon;
+    const uint16_t* src = raw.data();
+    if (r.kind == WK_LINEAR) {
+        // the reference stores Linear weights [in, out] (vk_engine.cpp:653, :629)
+        const int64_t out = r.shape[0], in = r.shape[1];
+        canon.resize((size_t)n);
+        for (int64_t i = 0; i < in; ++i)
+            for (int64_t o = 0; o < out; ++o) canon[(size_t)(o * in + i)] = raw[(size_t)(i * out + o)];
+        src = canon.data();
+    }
+    return upload_canonical_f16(c, r, src);
+}
+
 int init_weights_dir(Ctx& c, const std::string& dir) {
     for (const WeightRec& r : c.weights) {
-        const std::string path = dir + "/" + r.name + ".bin";
-        std::ifstream f(path, std::ios::binary | std::ios::ate);
-        if (!f) return set_err(&c, SDU_ERR_WEIGHT, "weight missing: " + path);
-        const int64_t sz = (int64_t)f.tellg();
-        const int64_t n = r.numel();
-        if (sz != n * 2)
-            return set_err(&c, SDU_ERR_WEIGHT, "weight size mismatch: " + path + " has " +
-                                                   std::to_string(sz) + " bytes, expected " +
-                                                   std::to_string(n * 2));
-        std::vector<uint16_t> raw((size_t)n);
-        f.seekg(0);
-        if (!f.read((char*)raw.data(), n * 2)) return set_err(&c, SDU_ERR_IO, "read failed: " + path);
-        std::vector<uint16_t> canon;
-        const uint16_t* src = raw.data();
-        if (r.kind == WK_LINEAR) {
-            // the reference stores Linear weights [in, out] (vk_engine.cpp:653, :629)
-            const int64_t out = r.shape[0], in = r.shape[1];
-            canon.resize((size_t)n);
-            for (int64_t i = 0; i < in; ++i)
-                for (int64_t o = 0; o < out; ++o) canon[(size_t)(o * in + i)] = raw[(size_t)(i * out + o)];
-            src = canon.data();
-        }
-        int st = upload_canonical_f16(c, r, src);
+        int st = load_weight_file(c, r, dir);
         if (st) return st;
     }
     return fold_weights(c);
+}
+
+int AuxNet::add(const std::string& name, std::vector<int64_t> shape, int kind, int layout, int ci_pad,
+                bool follows) {
+    WeightRec r;
+    r.name = name;
+    r.shape = std::move(shape);
+    r.kind = kind;
+    r.layout = layout;
+    r.ci_pad = ci_pad;
+    r.dev_n = layout == GL_CONV_OHWI ? r.shape[0] * r.shape[2] * r.shape[3] * ci_pad : r.numel();
+    widx[name] = (int)weights.size();
+    weights.push_back(r);
+    contig.push_back(follows ? 1 : 0);
+    return (int)weights.size() - 1;
+}
+
+int aux_alloc(Ctx& c, AuxNet& n, size_t extra_bytes) {
+    auto align = [](int64_t v) { return (v + 127) & ~(int64_t)127; };
+    std::vector<int64_t> off(n.weights.size());
+    int64_t top = 0;
+    for (size_t i = 0; i < n.weights.size(); ++i) {
+        if (n.contig[i] && i > 0) {
+            off[i] = off[i - 1] + n.weights[i - 1].dev_n;
+            top = std::max(top, align(off[i] + n.weights[i].dev_n));
+        } else {
+            off[i] = top;
+            top += align(n.weights[i].dev_n);
+        }
+    }
+    n.pool_bytes = (size_t)top * sizeof(f16) + extra_bytes;
+    if (hipMalloc(&n.pool, n.pool_bytes) != hipSuccess) return set_err(&c, SDU_ERR_OOM, "weight pool allocation failed");
+    for (size_t i = 0; i < n.weights.size(); ++i) n.weights[i].dev = n.pool + off[i];
+    return SDU_OK;
 }
 
 int set_weight_canonical(Ctx& c, const WeightRec& r, const float* data) {

@@ -66,6 +66,14 @@ inline void launch_timed(const char* kernel, double flops, double bytes, const F
 // sources (a 1x1 conv over another tensor of the same pixels, summed into the
 // same outputs).
 enum AMode { A_DENSE = 0, A_CONV3 = 1 };
+// Output activation of a GEMM / conv: none, ReLU (the TAESD decoder's convs and block
+// fuse) or quick-GELU x * sigmoid(1.702 x) (the CLIP text encoder's fc1).
+enum ActFn { ACT_NONE = 0, ACT_RELU = 1, ACT_QUICK_GELU = 2 };
+__device__ __forceinline__ float apply_act(int act, float v) {
+    if (act == ACT_RELU) return fmaxf(v, 0.f);
+    if (act == ACT_QUICK_GELU) return v / (1.0f + __expf(-1.702f * v));
+    return v;
+}
 enum OutMode { OUT_F16 = 0, OUT_F32 = 1, OUT_F32_NCHW = 2 };
 
 struct GemmArgs {
@@ -93,6 +101,7 @@ struct GemmArgs {
     int out_mode;
     int hw_out;         // OUT_F32_NCHW: pixels per image
     int geglu;
+    int act;            // activation on the final value (after bias, GEGLU, residual): ACT_*
     // split-K (set by gemm_launch).  fixup: each block of a tile stores its fp32
     // partial tile into the tile's slots and the last of them to arrive (per-tile
     // counter) sums the slots and runs the epilogue.  Otherwise the blocks store
@@ -148,6 +157,7 @@ struct AttnArgs {
     int B, heads, Sq, Sk, d;
     int ldq, ldk, ldv, ldo;
     float scale;
+    int causal;  // query i attends keys 0..i only (Sq == Sk; the CLIP text encoder)
 };
 hipError_t attention_launch(const AttnArgs& a, hipStream_t s);
 
@@ -170,9 +180,14 @@ hipError_t layernorm_launch(const f16* x, const f16* gamma, const f16* beta, f16
 
 // ----------------------------------------------------------------- elementwise
 // NCHW fp32 [Bsrc,C,H,W] -> NHWC fp16 [B,H,W,Cpad]; batch b reads source b % Bsrc,
-// channels >= C are zero.
+// channels >= C are zero.  tanh_clamp: each value becomes 3 tanh(x / 3) first (the
+// TAESD decoder's input clamp).
 hipError_t nchw_to_nhwc_launch(const float* src, f16* dst, int B, int Bsrc, int C, int Cpad, int HW,
-                               hipStream_t s);
+                               hipStream_t s, int tanh_clamp = 0);
+// Token + position embedding: out[b*S + i][:] = tok[ids[b*S + i]][:] + pos[i][:] (fp16,
+// summed in fp32), ids clamped to [0, vocab).  C % 8 == 0.
+hipError_t embed_launch(const int32_t* ids, const f16* tok, const f16* pos, f16* out, int B, int S, int C,
+                        int vocab, hipStream_t s);
 // fp32 -> fp16 copy
 hipError_t f32_to_f16_launch(const float* src, f16* dst, int64_t n, hipStream_t s);
 hipError_t f16_to_f32_launch(const f16* src, float* dst, int64_t n, hipStream_t s);

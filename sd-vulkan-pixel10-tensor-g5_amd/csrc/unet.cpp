@@ -5,7 +5,7 @@
 // the graph without launching to size the activation arena and workspaces, then
 // the real pass is captured into a HIP graph and replayed on later calls (the
 // reference records one command buffer per forward, :714, :783-788).
-#include "engine.h"
+#include "graph.h"
 
 #include <algorithm>
 #include <cmath>
@@ -25,98 +25,6 @@ static const int kLatC = 4, kLatCpad = 8, kCtxDim = 768;
 thread_local KernelTimer* g_kernel_timer = nullptr;
 thread_local hipEvent_t g_launch_ev0 = nullptr, g_launch_ev1 = nullptr;
 
-struct ProfRec {
-    std::string cat, kern, shape;
-    double flops, bytes;
-    hipEvent_t e0, e1;
-};
-
-// Times every kernel launch on its own: the launch goes through hipExtLaunchKernelGGL
-// with a start and a stop event of its own (SDU_LAUNCH), which record the start and end
-// of that kernel's execution.  Each kernel runs once, so the profiled pass computes the
-// same values as a forward.
-struct EventTimer : KernelTimer {
-    hipStream_t s;
-    std::string cat, shape;
-    std::vector<ProfRec> recs;
-    void run(const char* kernel, double flops, double bytes, void (*fn)(const void*), const void* arg) override {
-        ProfRec pr;
-        pr.cat = cat; pr.kern = kernel; pr.shape = shape;
-        pr.flops = flops; pr.bytes = bytes;
-        hipEventCreate(&pr.e0);
-        hipEventCreate(&pr.e1);
-        g_launch_ev0 = pr.e0;
-        g_launch_ev1 = pr.e1;
-        fn(arg);
-        g_launch_ev0 = g_launch_ev1 = nullptr;
-        recs.push_back(pr);
-    }
-};
-
-struct Exec {
-    Ctx& c;
-    hipStream_t s;
-    Arena* ar;
-    int B;
-    bool dry = false;
-    float* gemm_ws = nullptr;
-    size_t gemm_ws_need = 0;
-    double* gn_acc = nullptr;  // next free GroupNorm accumulator slot (zeroed per forward)
-    double* st_next = nullptr;  // per-channel output statistics pool (zeroed per forward)
-    double* st_end = nullptr;
-    hipError_t err = hipSuccess;
-    EventTimer* timer = nullptr;  // eager profiling only
-
-    template <class T>
-    T* alloc(size_t n) { return (T*)ar->alloc(n * sizeof(T)); }
-
-    // One op: `cat` names the op category; the kernels it launches report their own
-    // names, FLOPs and bytes to the timer when profiling.
-    template <class F>
-    void run(const char* cat, F&& launch, const std::string& shape = std::string()) {
-        if (dry || err != hipSuccess) return;
-        if (timer) { timer->cat = cat; timer->shape = shape; }
-        hipError_t e = launch();
-        if (e != hipSuccess) err = e;
-    }
-};
-
-static void gemm(Exec& E, const char* cat, const GemmArgs& a) {
-    const size_t ws = gemm_workspace_bytes(a);
-    if (ws > E.gemm_ws_need) E.gemm_ws_need = ws;
-    char shape[96];
-    snprintf(shape, sizeof shape, "%s M=%d N=%d K=%d geglu=%d", a.amode == A_CONV3 ? "conv3" : a.ln_colsum ? "dense_ln" : "dense",
-             a.M, a.N, a.K, a.geglu);
-    E.run(cat, [&] { return gemm_launch(a, E.gemm_ws, E.s); }, shape);
-}
-
-static GemmArgs dense_args(const f16* A, int lda, int M, int N, int K, const f16* W, void* C, int ldc) {
-    GemmArgs a{};
-    a.M = M; a.N = N; a.K = K;
-    a.amode = A_DENSE;
-    a.A = A; a.lda = lda; a.K1 = K;
-    a.Wt = W;
-    a.C = C; a.ldc = ldc;
-    a.out_mode = OUT_F16;
-    return a;
-}
-
-// 3x3 conv (pad 1) as implicit GEMM; returns output spatial size via Ho/Wo.
-static GemmArgs conv3_args(const f16* x, int B, int Hin, int Win, int Cin, int Cout, int stride,
-                           int ups, const f16* W, void* y) {
-    GemmArgs a{};
-    a.amode = A_CONV3;
-    a.A = x;
-    a.Bn = B; a.Hin = Hin; a.Win = Win; a.Cin = Cin;
-    a.stride = stride; a.upsample = ups;
-    a.Ho = ups ? 2 * Hin : (stride == 2 ? (Hin - 1) / 2 + 1 : Hin);
-    a.Wo = ups ? 2 * Win : (stride == 2 ? (Win - 1) / 2 + 1 : Win);
-    a.M = B * a.Ho * a.Wo; a.N = Cout; a.K = 9 * Cin;
-    a.Wt = W;
-    a.C = y; a.ldc = Cout;
-    a.out_mode = OUT_F16;
-    return a;
-}
 
 // An activation with, when its producing GEMM kept them, the per-channel sums and sums
 // of squares [B][C][2] of its values (for the GroupNorm that reads it).
@@ -564,9 +472,6 @@ void free_fwd_states(Ctx& c) {
     c.fwd.clear();
 }
 
-static int hip_fail(Ctx& c, hipError_t e, const char* what) {
-    return set_err(&c, SDU_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
-}
 
 // Plan a state: size (dry run), allocate, and capture the graph.
 static int plan_state(Ctx& c, FwdState& S) {

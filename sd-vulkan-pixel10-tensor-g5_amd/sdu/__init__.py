@@ -31,6 +31,9 @@ SDU_INIT_RANDOM_AFFINE = 0x1
 SDU_INIT_NO_WEIGHTS = 0x2
 SDU_EPI_GEGLU = 0x1
 SDU_EPI_OUT_F32 = 0x2
+SDU_EPI_RELU = 0x4
+SDU_EPI_QUICK_GELU = 0x8
+SDU_ATTN_CAUSAL = 0x1
 
 # every symbol include/sdu.h declares
 EXPORTS = [
@@ -39,8 +42,9 @@ EXPORTS = [
     "sdu_forward_device", "sdu_denoise_lcm_device", "sdu_denoise_lcm_ex", "sdu_selftest", "sdu_selftest_ex", "sdu_time_proj", "sdu_profile",
     "sdu_tensor_alloc", "sdu_tensor_free", "sdu_tensor_upload", "sdu_tensor_download",
     "sdu_tensor_device_ptr", "sdu_tensor_bytes", "sdu_groupnorm", "sdu_groupnorm_noalloc", "sdu_layernorm", "sdu_matmul",
-    "sdu_conv2d", "sdu_attention", "sdu_geglu", "sdu_silu", "sdu_add", "sdu_add_bias",
-    "sdu_lcm_step",
+    "sdu_conv2d", "sdu_attention", "sdu_attention_ex", "sdu_geglu", "sdu_silu", "sdu_add", "sdu_add_bias",
+    "sdu_lcm_step", "sdu_taesd_init", "sdu_taesd_decode", "sdu_taesd_decode_device", "sdu_clip_init",
+    "sdu_clip_encode", "sdu_clip_encode_device", "sdu_generate",
 ]
 
 
@@ -108,6 +112,14 @@ def load(path: str = LIB_PATH):
         "sdu_matmul": ([P, P, P, P, P, P, P, I, I, I, I, I], I),
         "sdu_conv2d": ([P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I], I),
         "sdu_attention": ([P, P, P, P, P, I, I, I, I, I, I, I, I, I, F], I),
+        "sdu_attention_ex": ([P, P, P, P, P, I, I, I, I, I, I, I, I, I, F, I], I),
+        "sdu_taesd_init": ([P, ctypes.c_char_p, ctypes.c_uint64, I], I),
+        "sdu_taesd_decode": ([P, P, I, I, I, P], I),
+        "sdu_taesd_decode_device": ([P, P, I, I, I, P], I),
+        "sdu_clip_init": ([P, ctypes.c_char_p, ctypes.c_uint64, I], I),
+        "sdu_clip_encode": ([P, P, I, P], I),
+        "sdu_clip_encode_device": ([P, P, I, P], I),
+        "sdu_generate": ([P, P, P, I, I, I, F, I, ctypes.c_uint64, P], I),
         "sdu_geglu": ([P, P, P, I, I], I),
         "sdu_silu": ([P, P, P, I64], I),
         "sdu_add": ([P, P, P, P, I64], I),
@@ -325,6 +337,46 @@ class Engine:
     def attention(self, q, k, v, o, B, heads, Sq, Sk, d, ldq, ldk, ldv, ldo, scale):
         self._check(load().sdu_attention(self.h, q.h, k.h, v.h, o.h, B, heads, Sq, Sk, d, ldq, ldk,
                                          ldv, ldo, scale))
+
+    def attention_ex(self, q, k, v, o, B, heads, Sq, Sk, d, ldq, ldk, ldv, ldo, scale, flags=0):
+        self._check(load().sdu_attention_ex(self.h, q.h, k.h, v.h, o.h, B, heads, Sq, Sk, d, ldq, ldk,
+                                            ldv, ldo, scale, flags))
+
+    # -- TAESD decoder, CLIP text encoder, end-to-end image -----------------
+    def taesd_init(self, weights_dir: Optional[str] = None, seed: int = 0, flags: int = 0):
+        self._check(load().sdu_taesd_init(self.h, weights_dir.encode() if weights_dir else None, seed, flags))
+
+    def taesd_decode(self, lat: np.ndarray) -> np.ndarray:
+        lat = np.ascontiguousarray(lat, np.float32)
+        B, _, H, W = lat.shape
+        out = np.empty((B, 3, 8 * H, 8 * W), np.float32)
+        self._check(load().sdu_taesd_decode(self.h, _ptr(lat), B, H, W, _ptr(out)))
+        return out
+
+    def taesd_decode_device(self, d_lat: int, B, H, W, d_img: int):
+        self._check(load().sdu_taesd_decode_device(self.h, d_lat, B, H, W, d_img))
+
+    def clip_init(self, weights_dir: Optional[str] = None, seed: int = 0, flags: int = 0):
+        self._check(load().sdu_clip_init(self.h, weights_dir.encode() if weights_dir else None, seed, flags))
+
+    def clip_encode(self, ids: np.ndarray) -> np.ndarray:
+        ids = np.ascontiguousarray(ids, np.int32)
+        B = ids.shape[0]
+        out = np.empty((B, 77, 768), np.float32)
+        self._check(load().sdu_clip_encode(self.h, _ptr(ids), B, _ptr(out)))
+        return out
+
+    def clip_encode_device(self, d_ids: int, B, d_out: int):
+        self._check(load().sdu_clip_encode_device(self.h, d_ids, B, d_out))
+
+    def generate(self, cond_ids, uncond_ids, H=64, W=64, steps=4, guidance=8.0, cfg_steps=None,
+                 seed=42) -> np.ndarray:
+        cond_ids = np.ascontiguousarray(cond_ids, np.int32)
+        uncond_ids = np.ascontiguousarray(uncond_ids, np.int32)
+        img = np.empty((3, 8 * H, 8 * W), np.float32)
+        self._check(load().sdu_generate(self.h, _ptr(cond_ids), _ptr(uncond_ids), H, W, steps, guidance,
+                                        steps if cfg_steps is None else cfg_steps, seed, _ptr(img)))
+        return img
 
     def geglu(self, g, y, T, C2):
         self._check(load().sdu_geglu(self.h, g.h, y.h, T, C2))
