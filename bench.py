@@ -98,6 +98,50 @@ def time_forward(eng, sdu, rng, B, H, W, L, steps, warmup, mark):
     return dt / steps * 1e3, d_out
 
 
+def time_image_path(eng, sdu, rng, reps):
+    """The networks around the UNet (seeded weights): CLIP text encoder on a prompt /
+    empty-prompt pair, the TAESD decoder on one 64x64 latent (-> 512x512 image), and the
+    whole sdu_generate call (CLIP, 4-step LCM + CFG at guidance 8, TAESD, host image out).
+    Device-resident inputs except for sdu_generate, whose token ids and image cross PCIe."""
+    import numpy as np
+    eng.clip_init(seed=5)
+    eng.taesd_init(seed=6)
+    ids = rng.integers(0, 49408, size=(2, 77)).astype(np.int32)
+    d_ids = eng.upload(ids.view(np.float32))  # raw int32 bits
+    d_ctx = eng.tensor((2, 77, 768), sdu.SDU_F32)
+    lat = rng.standard_normal((1, 4, 64, 64)).astype(np.float32)
+    d_lat = eng.upload(lat)
+    d_img = eng.tensor((1, 3, 512, 512), sdu.SDU_F32)
+
+    def timed(fn):
+        for _ in range(2):
+            fn()
+        eng.sync()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        eng.sync()
+        return (time.perf_counter() - t0) / reps * 1e3
+
+    clip_ms = timed(lambda: eng.clip_encode_device(d_ids.ptr, 2, d_ctx.ptr))
+    taesd_ms = timed(lambda: eng.taesd_decode_device(d_lat.ptr, 1, 64, 64, d_img.ptr))
+    gen_ms = timed(lambda: eng.generate(ids[0], ids[1], 64, 64, 4, 8.0, 4, 42))
+    # algorithmic work.  CLIP: 2 x 77 tokens, per layer QKV + out-proj (4 C^2) and the MLP
+    # (2 C 3072) per token, plus causal attention counted dense (4 B heads S^2 d).
+    T = 2 * 77
+    clip_flop = 12 * (2 * T * (4 * 768 * 768 + 2 * 768 * 3072) + 4 * 2 * 12 * 77 * 77 * 64)
+    # TAESD, 3x3 convs (2 * 9 * pixels * Cin * Cout): conv_in 4->64 and 9 block convs at 64^2,
+    # 10 convs (upsampling conv + 9 block convs) at 128^2 and at 256^2, 4 at 512^2, conv_out 64->3
+    taesd_flop = 2 * 9 * (64 * 64 * (4 * 64 + 9 * 64 * 64) + 128 * 128 * 10 * 64 * 64 + 256 * 256 * 10 * 64 * 64 +
+                          512 * 512 * (4 * 64 * 64 + 64 * 3))
+    return {"clip_encode_b2_ms": round(clip_ms, 3), "clip_tflops": round(clip_flop / clip_ms / 1e9, 1),
+            "taesd_decode_64x64_ms": round(taesd_ms, 3),
+            "taesd_tflops": round(taesd_flop / taesd_ms / 1e9, 1),
+            "taesd_frac_mfma": round(taesd_flop / taesd_ms / 1e9 / PEAK_MFMA_TFLOPS, 4),
+            "generate_512px_ms": round(gen_ms, 3), "generate_images_per_s": round(1e3 / gen_ms, 2),
+            "reps": reps, "weights": "seeded random (CLIP N(0,0.02), TAESD convs N(0,0.04))"}
+
+
 def measured_traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary
     (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by what the counter reads for
@@ -272,6 +316,7 @@ def main():
                                     "images_per_s": round(b * 1e3 / ms, 1), "steps": n,
                                     "roofline_ideal_ms": ideal, "frac_of_roofline": round(ideal / ms, 4)}
 
+    image_path = time_image_path(eng, sdu, rng, max(5, args.steps // 5))
     cpu = None if args.no_cpu else cpu_baseline()
     eng.release()
 
@@ -299,6 +344,7 @@ def main():
         "profile_total_ms": round(prof_total, 4),
         "kernels": per_kernel,
         "categories": per_cat,
+        "image_path": image_path,
     }
     print(json.dumps(line), flush=True)
 

@@ -134,8 +134,10 @@ def test_taesd_decode_matches_oracle(taesd_engine, B, H, W):
     with torch.inference_mode():
         ref = taesd_ref.decode(p, z).numpy()
     assert got.shape == (B, 3, 8 * H, 8 * W)
-    err = rel_err_l1(got, ref)
-    say(f"  relErr_L1 {err:.2e}")
+    # compared before the output affine y = 2 x - 1: its constant -1 would dilute the
+    # error of the network itself
+    err = rel_err_l1(got + 1.0, ref + 1.0)
+    say(f"  relErr_L1 of y + 1 {err:.2e} (of y {rel_err_l1(got, ref):.2e})")
     assert err < 3e-3
     # replay of the captured graph is deterministic
     np.testing.assert_array_equal(taesd_engine.taesd_decode(z), got)
