@@ -271,14 +271,23 @@ void gemm_kernel(GemmArgs a) {
     const int wm = wave % WM, wn = wave / WM;
 
     // XCD-aware block order: consecutive hardware block ids go round-robin over the
-    // 8 XCDs; give each XCD a contiguous range of logical tiles so neighbouring
-    // tiles (same A rows) share that XCD's L2.
+    // 8 XCDs; give each XCD a contiguous range of logical tiles (XCD x: the nblk / 8
+    // tiles, one more for the first nblk % 8 XCDs, after those of XCDs < x), so that
+    // neighbouring tiles share that XCD's L2.  Neighbours share A rows (M-major order)
+    // or, when the weights are the larger operand, W columns (N-major order).
     const int tiles_n = (a.N + NT - 1) / NT;
     const int tiles_m = (a.M + MT - 1) / MT;
     const int nblk = tiles_m * tiles_n;
-    int bid = blockIdx.x;
-    if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
-    const int tm = bid / tiles_n, tn = bid - tm * tiles_n;
+    const int xcd = blockIdx.x & 7, per = nblk >> 3, extra = nblk & 7;
+    const int bid = xcd * per + min(xcd, extra) + (blockIdx.x >> 3);
+    int tm, tn;
+    if (a.n_major) {
+        tn = bid / tiles_m;
+        tm = bid - tn * tiles_m;
+    } else {
+        tm = bid / tiles_n;
+        tn = bid - tm * tiles_n;
+    }
     const int m0 = tm * MT, n0 = tn * NT;
 
     const int kbeg = blockIdx.z * a.k_per_split;
@@ -1080,6 +1089,14 @@ hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s) {
     a.splits = splits;
     a.k_per_split = kps;
     a.fixup = fix;
+    // tile order: N-major when the weights outweigh the A source (a conv's A is its input
+    // image, whose 9 taps hit the same L2 lines)
+    {
+        const double w_b = 2.0 * a.N * a.K;
+        const double a_b = a.amode == A_CONV3 ? 2.0 * a.Bn * a.Hin * a.Win * a.Cin + 2.0 * a.M * (a.K - a.K1)
+                                              : 2.0 * a.M * a.K;
+        a.n_major = w_b > a_b;
+    }
     a.tile_cnt = splits > 1 ? (unsigned*)ws : nullptr;
     a.partial = splits > 1 ? (float*)((char*)ws + kCounterBytes) : nullptr;
     if (splits > 1 && ws == nullptr) return hipErrorInvalidValue;

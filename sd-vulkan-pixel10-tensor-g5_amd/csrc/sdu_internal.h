@@ -110,6 +110,7 @@ struct GemmArgs {
     unsigned* tile_cnt; // fixup: [tiles] arrival counters, zero on entry and left zero
     int fixup;
     int splits;
+    int n_major;        // tile order (set by gemm_launch): N-major when W is the larger operand
     int k_per_split;    // multiple of the K tile
     // Optional per-channel statistics of the stored fp16 output, for a GroupNorm that
     // reads it: stats[b][n] += (sum, sum of squares) over the rows m of image
