@@ -287,6 +287,14 @@ def main():
         ach = dom["bytes"] / (dom["ms"] * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(ach / PEAK_HBM_GBS, 4)}
+    # the box's measured ceilings (sdu_calibrate): register-only MFMA under sustained load
+    # (with the shader clock it runs at) and a 16-byte streaming copy
+    cal = eng.calibrate(512)
+    cal = {k: round(v, 3) for k, v in cal.items()}
+    if roof["unit"] == "TFLOP/s":
+        roof["frac_of_measured_mfma_peak"] = round(roof["achieved"] / cal["mfma_tflops"], 4)
+    else:
+        roof["frac_of_measured_copy"] = round(roof["achieved"] / cal["copy_gbs"], 4)
     traffic = measured_traffic(dom_name)
     roof.update({"traffic": traffic, "kernel": dom_name, "calls": dom["calls"],
                  "timing": "start/stop HIP events of each launch (hipExtLaunchKernelGGL) on the engine "
@@ -340,6 +348,9 @@ def main():
         "other_shapes": extra,
         "host_io_forwards_per_s": round(host_fps, 3),
         "roofline": roof,
+        "calibration": dict(cal, note="sdu_calibrate on this box: dense f16 MFMA from registers on all "
+                                      "CUs (and the shader clock during it), 16-byte streaming copy of "
+                                      "512 MiB (read + write)"),
         "cpu_baseline": cpu,
         "profile_total_ms": round(prof_total, 4),
         "kernels": per_kernel,

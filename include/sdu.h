@@ -180,6 +180,18 @@ int sdu_selftest_ex(sdu_ctx* ctx, const char* fixture_dir, sdu_selftest_report* 
  * kernel's own execution on the context stream (hipExtLaunchKernelGGL), and runs once.
  * Entries are accumulated per op category (e.g. "conv3x3") and per kernel ("k:" +
  * kernel name, e.g. "k:gemm_kernel<128,128,2,2,64,2>"); total_ms sums the categories. */
+/* The GPU's practical ceilings, measured like the reference's micro-benchmarks
+ * (VulkanBench.kt:10-19, benchMatmul / benchSilu ...) time single shaders: dense f16 MFMA
+ * from registers on every CU (TFLOP/s, and the shader clock during that load), and a
+ * 16-byte streaming device copy of copy_mib MiB (read + write GB/s).  Allocates and frees
+ * 2 x copy_mib MiB; takes about 0.1 s. */
+typedef struct sdu_calibration {
+    double mfma_tflops;
+    double mfma_clock_ghz;
+    double copy_gbs;
+} sdu_calibration;
+int sdu_calibrate(sdu_ctx* ctx, int copy_mib, sdu_calibration* out);
+
 typedef struct sdu_prof_entry {
     char name[48];
     int calls;

@@ -485,6 +485,52 @@ double sdu_selftest(sdu_ctx* ctx, const char* fixture_dir) {
     return std::max(r.relerr_b1, std::max(r.relerr_b2[0], r.relerr_b2[1]));
 }
 
+int sdu_calibrate(sdu_ctx* ctx, int copy_mib, sdu_calibration* out) {
+    SDU_GUARD(ctx);
+    if (!out || copy_mib < 16 || copy_mib > 8192) return fail(ctx, SDU_ERR_ARG, "copy_mib in 16..8192");
+    return guarded(ctx, [&]() -> int {
+        hipStream_t s = ctx->c.stream;
+        const size_t bytes = (size_t)copy_mib << 20;
+        char* buf = nullptr;
+        float* sink = nullptr;
+        long long* clk = nullptr;
+        hipEvent_t e0 = nullptr, e1 = nullptr;
+        hipError_t e = hipMalloc(&buf, 2 * bytes);
+        if (e == hipSuccess) e = hipMalloc(&sink, 512 * sizeof(float) + 2 * sizeof(long long));
+        if (e != hipSuccess) {
+            hipFree(buf);
+            return fail(ctx, SDU_ERR_OOM, "calibration buffers");
+        }
+        clk = (long long*)(sink + 512);
+        const int blocks = 4 * 256, iters = 10000;
+        float ms_mfma = 0.f, ms_copy = 0.f;
+        long long ck[2] = {0, 0};
+        if ((e = hipEventCreate(&e0)) || (e = hipEventCreate(&e1)) ||
+            (e = hipMemsetAsync(buf, 0, 2 * bytes, s)) ||
+            (e = mfma_probe_launch(sink, clk, blocks, iters / 10, s)) ||  // warm-up
+            (e = hipEventRecord(e0, s)) || (e = mfma_probe_launch(sink, clk, blocks, iters, s)) ||
+            (e = hipEventRecord(e1, s)) || (e = hipEventSynchronize(e1)) || (e = hipEventElapsedTime(&ms_mfma, e0, e1)) ||
+            (e = hipMemcpy(ck, clk, sizeof ck, hipMemcpyDeviceToHost)) ||
+            (e = copy_probe_launch(buf, buf + bytes, bytes, s)) ||  // warm-up
+            (e = hipEventRecord(e0, s)))
+            goto done;
+        for (int r = 0; r < 10 && e == hipSuccess; ++r) e = copy_probe_launch(buf, buf + bytes, bytes, s);
+        if (e == hipSuccess && !(e = hipEventRecord(e1, s)) && !(e = hipEventSynchronize(e1)))
+            e = hipEventElapsedTime(&ms_copy, e0, e1);
+    done:
+        hipStreamSynchronize(s);
+        if (e0) hipEventDestroy(e0);
+        if (e1) hipEventDestroy(e1);
+        hipFree(buf);
+        hipFree(sink);
+        if (e != hipSuccess) return hipfail(ctx, e, "calibrate");
+        out->mfma_tflops = (double)blocks * 8 * iters * 16 * 32768.0 / (ms_mfma * 1e-3) / 1e12;
+        out->mfma_clock_ghz = ck[1] > 0 ? (double)ck[0] / ((double)ck[1] * 10.0) : 0.0;
+        out->copy_gbs = 2.0 * bytes * 10 / (ms_copy * 1e-3) / 1e9;
+        return SDU_OK;
+    });
+}
+
 int sdu_time_proj(int t, float* out) {
     if (!out || t < 0 || t > 100000) return fail(nullptr, SDU_ERR_ARG, "bad time_proj argument");
     time_proj_host(t, out);

@@ -242,6 +242,12 @@ hipError_t fold_shortcut_launch(const f16* w2, const f16* b2, const f16* ws, con
 // n fp32 N(0,1) values of the same generator (element i from key, no fp16 rounding).
 hipError_t gen_normal_f32_launch(float* dst, int64_t n, uint64_t key, hipStream_t s);
 
+// Calibration (k_probe.hip): `blocks` x 8 waves of register-only f16 MFMA, `iters` x 16 per
+// wave; clk[0] / clk[1] = shader-clock / 100 MHz real-time ticks of block 0's loop; sink
+// >= 512 floats (never written in practice).  A 16-byte streaming copy of `bytes`.
+hipError_t mfma_probe_launch(float* sink, long long* clk, int blocks, int iters, hipStream_t s);
+hipError_t copy_probe_launch(const void* src, void* dst, size_t bytes, hipStream_t s);
+
 uint64_t fnv1a64(const char* s);
 uint64_t splitmix64(uint64_t x);
 

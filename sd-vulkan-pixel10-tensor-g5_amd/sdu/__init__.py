@@ -44,7 +44,7 @@ EXPORTS = [
     "sdu_tensor_device_ptr", "sdu_tensor_bytes", "sdu_groupnorm", "sdu_groupnorm_noalloc", "sdu_layernorm", "sdu_matmul",
     "sdu_conv2d", "sdu_attention", "sdu_attention_ex", "sdu_geglu", "sdu_silu", "sdu_add", "sdu_add_bias",
     "sdu_lcm_step", "sdu_taesd_init", "sdu_taesd_decode", "sdu_taesd_decode_device", "sdu_clip_init",
-    "sdu_clip_encode", "sdu_clip_encode_device", "sdu_generate",
+    "sdu_clip_encode", "sdu_clip_encode_device", "sdu_generate", "sdu_calibrate",
 ]
 
 
@@ -57,6 +57,11 @@ class SduError(RuntimeError):
 class SelftestReport(ctypes.Structure):
     _fields_ = [("relerr_b1", ctypes.c_double), ("relerr_b2", ctypes.c_double * 2),
                 ("ctx_sens", ctypes.c_double)]
+
+
+class Calibration(ctypes.Structure):
+    _fields_ = [("mfma_tflops", ctypes.c_double), ("mfma_clock_ghz", ctypes.c_double),
+                ("copy_gbs", ctypes.c_double)]
 
 
 class ProfEntry(ctypes.Structure):
@@ -120,6 +125,7 @@ def load(path: str = LIB_PATH):
         "sdu_clip_encode": ([P, P, I, P], I),
         "sdu_clip_encode_device": ([P, P, I, P], I),
         "sdu_generate": ([P, P, P, I, I, I, F, I, ctypes.c_uint64, P], I),
+        "sdu_calibrate": ([P, I, ctypes.POINTER(Calibration)], I),
         "sdu_geglu": ([P, P, P, I, I], I),
         "sdu_silu": ([P, P, P, I64], I),
         "sdu_add": ([P, P, P, P, I64], I),
@@ -300,6 +306,12 @@ class Engine:
             e = arr[i]
             out[e.name.decode()] = dict(calls=e.calls, ms=e.ms, flops=e.flops, bytes=e.bytes)
         return out, tot.value
+
+    def calibrate(self, copy_mib: int = 512) -> dict:
+        """sdu_calibrate: measured MFMA ceiling, shader clock under it, streaming-copy GB/s."""
+        r = Calibration()
+        self._check(load().sdu_calibrate(self.h, copy_mib, ctypes.byref(r)))
+        return {"mfma_tflops": r.mfma_tflops, "mfma_clock_ghz": r.mfma_clock_ghz, "copy_gbs": r.copy_gbs}
 
     # -- tensors and ops -------------------------------------------------
     def tensor(self, shape, dtype=SDU_F16) -> Tensor:

@@ -241,3 +241,16 @@ def test_generate_is_the_device_chain(unet_engine):
     assert err <= 1e-4
     np.testing.assert_array_equal(eng.generate(cond, unc, H, W, steps, guidance, steps, seed), img)
     assert rel_err_l1(eng.generate(cond, unc, H, W, steps, guidance, steps, seed + 1), img) > 1e-3
+
+
+# ------------------------------------------------------------------ calibration
+
+
+def test_calibrate_sane(op_engine):
+    """sdu_calibrate reports the box's MFMA ceiling, the shader clock under it and a copy
+    rate; each within what an MI355X can physically do (2.5 PF/s, 2.4 GHz, 8 TB/s)."""
+    c = op_engine.calibrate(64)
+    say(f"calibration {c}")
+    assert 300.0 < c["mfma_tflops"] <= 2600.0
+    assert 0.5 < c["mfma_clock_ghz"] <= 2.5
+    assert 500.0 < c["copy_gbs"] <= 8200.0
