@@ -480,17 +480,20 @@ static void launch_cfg(const AttnArgs& a, hipStream_t s) {
     const double bytes = 2.0 * bh * a.d * (2.0 * a.Sq + 2.0 * a.Sk);
     char name[48];
     // shared K/V tiles where there are enough query waves to fill the chip (the
-    // key-split kernel re-reads K/V per wave); two waves per block when four would
-    // leave < 512 blocks.  Fewer query waves (e.g. 1024 queries x 16 heads), and short
-    // key sequences (cross-attention over the 77 context tokens), go to the key-split
-    // kernel: its extra waves, or not staging a few K/V tiles per block, win.
+    // key-split kernel re-reads K/V per wave): four query waves per block, eight for
+    // heads of 56..128 when four would leave < 512 blocks (their larger K/V tiles are
+    // then shared by more waves; measured per shape: d80 at 2304 tokens, B=2, 0.43 ms
+    // with two waves, 0.375 with four, 0.353 with eight; d160 at 256 tokens, B=16, 0.221
+    // with two, 0.158 with four).  Fewer query waves (e.g. 1024 queries x 16 heads), and
+    // short key sequences (cross-attention over the 77 context tokens), go to the
+    // key-split kernel: its extra waves, or not staging a few K/V tiles per block, win.
     if (qwaves >= 1024 && a.Sk > 128 && !a.causal) {
-        const int nw = ((a.Sq + 127) / 128) * bh >= 512 ? 4 : 2;
+        const int nw = (a.d > 48 && a.d <= 128 && ((a.Sq + 127) / 128) * bh < 512) ? 8 : 4;
         snprintf(name, sizeof name, "attn_kernel<%d,%d,%d,%d>", KS, MTD, nw, (int)LSUM);
         const dim3 grid((a.Sq + nw * 32 - 1) / (nw * 32), a.heads, a.B);
         launch_timed(name, flops, bytes, [&] {
-            if (nw == 4) SDU_LAUNCH((attn_kernel<KS, MTD, 4, LSUM>), grid, dim3(256), 0, s, a);
-            else SDU_LAUNCH((attn_kernel<KS, MTD, 2, LSUM>), grid, dim3(128), 0, s, a);
+            if (nw == 8) SDU_LAUNCH((attn_kernel<KS, MTD, 8, LSUM>), grid, dim3(512), 0, s, a);
+            else SDU_LAUNCH((attn_kernel<KS, MTD, 4, LSUM>), grid, dim3(256), 0, s, a);
         });
         return;
     }

@@ -231,6 +231,8 @@ def test_conv2d(op_engine, B, H, W, Ci, Co, k, stride, ups, temb, res):
     (2, 8, 4096, 4096, 40),   # level-0 self-attention
     (2, 8, 4096, 77, 40),     # level-0 cross-attention
     (2, 8, 1024, 1024, 80),
+    (2, 8, 2304, 2304, 80),   # 96x96 level-1 self-attention: eight query waves per block
+    (16, 8, 256, 256, 160),   # B=16 level-2 self-attention: shared K/V tiles, four waves
     (2, 8, 256, 256, 160),
     (2, 8, 64, 64, 160),      # mid block
     (2, 8, 256, 77, 160),
