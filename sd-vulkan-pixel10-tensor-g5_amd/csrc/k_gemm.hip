@@ -1129,9 +1129,14 @@ hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s) {
     });
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || splits == 1 || fix) return e;
+    return splitk_reduce_launch(a, part_bytes + out_bytes, s);
+}
+
+hipError_t splitk_reduce_launch(const GemmArgs& a, double bytes, hipStream_t s) {
+    const int nout = a.geglu ? a.N / 2 : a.N;
     const bool vec = a.out_mode != OUT_F32_NCHW && (a.N & 7) == 0;
     const int64_t total = (int64_t)a.M * (vec ? nout / 8 : nout);
-    launch_timed("splitk_reduce_kernel", 0.0, part_bytes + out_bytes, [&] {
+    launch_timed("splitk_reduce_kernel", 0.0, bytes, [&] {
         SDU_LAUNCH(splitk_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, a);
     });
     return hipGetLastError();

@@ -146,6 +146,8 @@ size_t gemm_counter_bytes();
 size_t gemm_workspace_bytes(const GemmArgs& a);
 const char* gemm_kernel_name(const GemmArgs& a);  // tile variant the launch will use
 hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s);
+// Sum a.splits fp32 partials [splits][M][N] at a.partial and run the epilogue.
+hipError_t splitk_reduce_launch(const GemmArgs& a, double bytes, hipStream_t s);
 
 // y[n] = act_out( sum_k act_in(x[k]) * W[n,k] + bias[n] ), fp32 in/out, W fp16 [N,K].
 // act: 0 none, 1 SiLU.

@@ -120,6 +120,11 @@ def test_layernorm(op_engine, T, C):
     (100, 128, 128, 0, True, False, True, False),     # GEGLU with ragged M
     (64, 64, 8192, 0, True, True, False, False),      # one tile, many K splits
     (200, 384, 3000, 0, True, False, False, True),    # split-K, ragged M and K tail, fp32 out
+    # few rows (the 8x8 level, batch 1 and 2): two sources along K, ragged M
+    (128, 1280, 6400, 1280, True, True, False, False),  # mid FF out + proj_out over [g | t]
+    (96, 320, 640, 0, True, True, False, True),          # ragged M, fp32 out
+    (64, 1280, 1280, 0, False, True, False, False),      # M = 64
+    (33, 64, 128, 0, True, False, True, False),          # ragged M, GEGLU
 ])
 def test_matmul(op_engine, M, N, K, K2, bias, res, geglu, f32):
     say(f"matmul M={M} N={N} K={K} K2={K2} bias={bias} res={res} geglu={geglu} f32={f32}")
@@ -191,6 +196,9 @@ def test_matmul_split_repeat(op_engine):
     (1, 5, 7, 16, 24, 3, 1, False, False, False),      # ragged
     (1, 5, 7, 16, 24, 3, 2, False, False, False),      # ragged stride 2
     (2, 32, 32, 640, 640, 1, 1, False, False, True),   # 1x1 proj
+    (2, 16, 16, 1280, 1280, 3, 2, False, False, False),  # downsample to 8x8 (M = 128)
+    (1, 8, 8, 640, 320, 3, 1, False, True, True),      # M = 64
+    (1, 6, 10, 128, 96, 3, 1, False, False, True),     # ragged M = 60, Cin = 128
 ])
 def test_conv2d(op_engine, B, H, W, Ci, Co, k, stride, ups, temb, res):
     say(f"conv2d B={B} {H}x{W} {Ci}->{Co} k={k} s={stride} ups={ups} temb={temb} res={res}")
