@@ -247,6 +247,11 @@ def test_conv2d(op_engine, B, H, W, Ci, Co, k, stride, ups, temb, res):
     (1, 2, 100, 37, 40),      # ragged query / key counts
     (1, 1, 1, 1, 8),          # single token
     (1, 3, 130, 200, 64),
+    # other head sizes: the ones row of V^T (row sums) at dims 24, 56, 120; none at 96
+    (1, 2, 70, 90, 24),
+    (1, 1, 33, 65, 56),
+    (1, 2, 40, 50, 96),
+    (1, 1, 20, 30, 120),
 ])
 def test_attention(op_engine, B, heads, Sq, Sk, d):
     say(f"attention B={B} heads={heads} Sq={Sq} Sk={Sk} d={d}")
