@@ -124,13 +124,15 @@ __device__ __forceinline__ void vt_pad_rows(f16* vt, int vstr, int keys, int d, 
 
 // ----------------------------------------------------------------- shared-tile kernel
 
-static constexpr int KT = 64;        // keys per iteration
-static constexpr int VSTR = KT + 8;  // Vt row stride (halves)
 
 // KS: 16-wide k-steps covering d for QK^T; MTD: 32-row dim tiles for PV;
-// NWAVE: waves per block (32 queries each; they share the K/V tiles in LDS).
-template <int KS, int MTD, int NWAVE, bool LSUM>
+// NWAVE: waves per block (32 queries each; they share the K/V tiles in LDS);
+// KT: keys per iteration (64, or 128 for small heads on grids of at most two blocks
+// per CU: half the barriers and per-tile softmax overhead per key).
+template <int KS, int MTD, int NWAVE, bool LSUM, int KT = 64>
 __global__ __launch_bounds__(NWAVE * 64) void attn_kernel(AttnArgs a) {
+    constexpr int VSTR = KT + 8;  // Vt row stride (halves)
+    constexpr int NSUB = KT / 32;
     constexpr int KSTR = KS * 16 + 8;  // K row stride (halves)
     constexpr int NTH = NWAVE * 64;
     __shared__ __attribute__((aligned(16))) f16 Ks[2][KT * KSTR];
@@ -262,9 +264,9 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_kernel(AttnArgs a) {
         if (it + 1 < nt) load_kv(kb + KT);
         __builtin_amdgcn_s_setprio(1);
 
-        floatx16 s[2];
+        floatx16 s[NSUB];
 #pragma unroll
-        for (int sub = 0; sub < 2; ++sub) {
+        for (int sub = 0; sub < NSUB; ++sub) {
             s[sub] = floatx16{};
             const f16* krow = &Ks[buf][(sub * 32 + key_perm(lrow)) * KSTR + lk];
 #pragma unroll
@@ -273,7 +275,7 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_kernel(AttnArgs a) {
                 s[sub] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], s[sub], 0, 0, 0);
             }
         }
-        softmax_pv<2, MTD, LSUM>(s, min(KT, a.Sk - kb), c, m_run, l_run, o, Vt[buf], VSTR, hl, lrow, lk);
+        softmax_pv<NSUB, MTD, LSUM>(s, min(KT, a.Sk - kb), c, m_run, l_run, o, Vt[buf], VSTR, hl, lrow, lk);
         __builtin_amdgcn_s_setprio(0);
         if (it + 1 < nt) store_kv(buf ^ 1);
         __syncthreads();
@@ -489,10 +491,15 @@ static void launch_cfg(const AttnArgs& a, hipStream_t s) {
     // key-split kernel: its extra waves, or not staging a few K/V tiles per block, win.
     if (qwaves >= 1024 && a.Sk > 128 && !a.causal) {
         const int nw = (a.d > 48 && a.d <= 128 && ((a.Sq + 127) / 128) * bh < 512) ? 8 : 4;
-        snprintf(name, sizeof name, "attn_kernel<%d,%d,%d,%d>", KS, MTD, nw, (int)LSUM);
         const dim3 grid((a.Sq + nw * 32 - 1) / (nw * 32), a.heads, a.B);
+        // 128-key tiles for heads <= 48 when every block is resident at once (two per CU):
+        // d40 at 4096 tokens, B=2, 0.44 ms per forward against 0.46 with 64-key tiles;
+        // on larger grids they lose (0.24 ms more at 9216 tokens, 0.31 ms at B=16)
+        const bool kt128 = KS == 3 && nw == 4 && (long)grid.x * bh <= 512;
+        snprintf(name, sizeof name, "attn_kernel<%d,%d,%d,%d%s>", KS, MTD, nw, (int)LSUM, kt128 ? ",128" : "");
         launch_timed(name, flops, bytes, [&] {
             if (nw == 8) SDU_LAUNCH((attn_kernel<KS, MTD, 8, LSUM>), grid, dim3(512), 0, s, a);
+            else if (KS == 3 && kt128) SDU_LAUNCH((attn_kernel<KS, MTD, 4, LSUM, (KS == 3 ? 128 : 64)>), grid, dim3(256), 0, s, a);
             else SDU_LAUNCH((attn_kernel<KS, MTD, 4, LSUM>), grid, dim3(256), 0, s, a);
         });
         return;
