@@ -947,9 +947,14 @@ struct Cfg {
 // 1: 128x128, 8 waves of 64x32, BK 64, 2-stage ring (64 KB: two per CU, 4 waves per SIMD)
 // 2: 128x64,  8 waves of 32x32, BK 64, 3-stage ring (72 KB: two per CU, 4 waves per SIMD)
 // Rates and fixed costs from dense GEMMs that give every CU one or two blocks, at
-// K = 512 and 4096 (the difference gives the rate, the rest the fixed cost).
+// K = 512 and 4096 (the difference gives the rate, the rest the fixed cost).  The
+// 128x128 two-block rate is set above that fit (3.54): the 64x64 convs over the up
+// path's concatenated inputs run two splits as co-resident pairs faster than it
+// predicts (640 -> 320: 56.6 us with 2 splits against 62.4 with 4), and whole forwards
+// compared in one call take 5.09 against 5.10 ms (B=2 64x64), 9.69 against 9.78 (96x96)
+// and 21.45 against 21.45 (B=16).
 const Cfg kCfgs[3] = {{256, 128, 1, 3.5e12, 3.5e12, 4.5e-6},
-                      {128, 128, 2, 2.76e12, 3.54e12, 3.0e-6},
+                      {128, 128, 2, 2.76e12, 3.9e12, 3.0e-6},
                       {128, 64, 2, 2.23e12, 3.03e12, 2.5e-6}};
 // full kernel names (tile configuration, then the A mode: 0 dense, 1 implicit conv)
 const char* const kNames[3][2] = {{"gemm_kernel<256,128,4,2,64,2,0>", "gemm_kernel<256,128,4,2,64,2,1>"},
