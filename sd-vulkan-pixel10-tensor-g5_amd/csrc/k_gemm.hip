@@ -27,6 +27,7 @@ namespace sdu {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 
@@ -86,14 +87,17 @@ __device__ __forceinline__ void stats_flush(const GemmArgs& a, const float (&st)
     __syncthreads();
     const int nslot = m_last / a.stats_hw != b0 ? 2 : 1;
     // value v of chunk c: slot v / 16, sum (0) or sum of squares (1) = (v / 8) % 2, column v % 8
-    static_assert(CPR * 32 <= NTH, "one value per thread");
-    const int c = tid >> 5, v = tid & 31;
-    const int col = col0 + c * 8 + (v & 7);
-    if (tid >= CPR * 32 || (v >> 4) >= nslot || col >= a.N) return;
-    float t = 0.f;
+    // (thread t owns chunk t % CPR; threads past the last whole group of CPR kept zeros)
 #pragma unroll
-    for (int j = 0; j < NTH / CPR; ++j) t += red[(c + j * CPR) * 32 + v];
-    atomicAdd(&a.stats[((int64_t)(b0 + (v >> 4)) * a.N + col) * 2 + ((v >> 3) & 1)], (double)t);
+    for (int q = tid; q < CPR * 32; q += NTH) {
+        const int c = q >> 5, v = q & 31;
+        const int col = col0 + c * 8 + (v & 7);
+        if ((v >> 4) >= nslot || col >= a.N) continue;
+        float t = 0.f;
+#pragma unroll
+        for (int j = 0; j < NTH / CPR; ++j) t += red[(c + j * CPR) * 32 + v];
+        atomicAdd(&a.stats[((int64_t)(b0 + (v >> 4)) * a.N + col) * 2 + ((v >> 3) & 1)], (double)t);
+    }
 }
 
 // Sum split-K partials and apply the epilogue.  Vector path: 8 output columns
@@ -247,12 +251,22 @@ __device__ __forceinline__ int lds_swizzle(int row) {
 
 // Two blocks per CU (4 waves per SIMD) where the ring leaves LDS for two: the
 // register budget is then 128 VGPRs.
-template <int MT, int NT, int WM, int WN, int BKT, int NS, int AM>
-__global__ __launch_bounds__(WM* WN * 64) __attribute__((amdgpu_waves_per_eu(MT == 256 ? 2 : 4)))
+//
+// MF: the MFMA, v_mfma_f32_32x32x16_f16 (32) or v_mfma_f32_16x16x32_f16 (16).  The 16x16
+// form lets a wave tile be an odd number of 16-column blocks: the 64x160 tile (4 waves of
+// 32x80) covers N = 320 in two tiles with no padded column and gives M = 8192 exactly 256
+// tiles, one per CU.  Its lane layout: A / B operand lane l, row / column l % 16, K
+// elements 8 (l / 16) .. + 8 of a 32-deep k-step; accumulator element e of lane l: row
+// 4 (l / 16) + e, column l % 16.  With MF 16 the wave tile is 32 rows (one epilogue pass).
+template <int MT, int NT, int WM, int WN, int BKT, int NS, int AM, int MF = 32>
+__global__ __launch_bounds__(WM* WN * 64) __attribute__((amdgpu_waves_per_eu(MT == 256 || MF == 16 ? 2 : 4)))
 void gemm_kernel(GemmArgs a) {
     constexpr int NW = WM * WN, NTH = NW * 64;
     constexpr int TMW = MT / WM, TNW = NT / WN;  // wave tile
-    constexpr int FM = TMW / 32, FN = TNW / 32;   // 32x32 MFMA tiles per wave
+    static_assert(MF == 32 || (MF == 16 && TMW == 32 && TNW % 16 == 0), "16x16 MFMA wave tile");
+    constexpr int FM = MF == 32 ? TMW / 32 : 1;   // 32-row epilogue passes per wave
+    constexpr int FN = MF == 32 ? TNW / 32 : 1;   // 32x32 MFMA tiles per wave row (MF 32)
+    constexpr int FM16 = TMW / 16, FN16 = TNW / 16;  // 16x16 MFMA tiles per wave (MF 16)
     constexpr int CPR = BKT / 8;                  // 16-byte chunks per LDS row
     constexpr int RPI = 1024 / (BKT * 2);         // rows one wave DMA instruction fills
     constexpr int AI = MT / RPI / NW, BI = NT / RPI / NW;  // DMA instructions per thread per tile
@@ -450,7 +464,9 @@ void gemm_kernel(GemmArgs a) {
     // under the K loop; otherwise per pass in the epilogue.  Only a block that runs
     // the epilogue loads them; no block writes output rows another block reads here.
     constexpr int PR = WM * 32;                // staged rows per pass
-    constexpr int MAXR = PR * (NT / 8) / NTH;  // staged rows per thread per pass (non-GEGLU)
+    // staged rows per thread per pass (non-GEGLU): the threads of one staged row are the
+    // NT / 8 chunk owners, NTH / (NT / 8) rows go per step
+    constexpr int MAXR = (PR + NTH / (NT / 8) - 1) / (NTH / (NT / 8));
     const bool narrow = a.out_mode == OUT_F32_NCHW || (a.N & 7);
     const int NTO = NT / (a.geglu ? 2 : 1);  // output columns of this tile
     const int cpr = NTO / 8;                  // 8-column chunks per row
@@ -460,6 +476,9 @@ void gemm_kernel(GemmArgs a) {
     const int n = n0 + tc;
     const int nout = a.geglu ? (n0 >> 1) + oc : n;
     constexpr bool PRE = FM * MAXR <= 2;
+    // (with a tile width whose 8-column chunks do not divide the thread count, the
+    // threads past the last whole row group stay out of the vector epilogue)
+    const bool ep_on = tid < rstep * cpr;
     const bool use_res = a.res && !narrow && n < a.N && (!a.partial || a.fixup);
     uint4 rres[FM][MAXR];
     auto load_res = [&](int ip) __attribute__((always_inline)) {
@@ -481,6 +500,11 @@ void gemm_kernel(GemmArgs a) {
     for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = floatx16{};
+    floatx4 acc16[MF == 16 ? FM16 : 1][MF == 16 ? FN16 : 1];
+#pragma unroll
+    for (int i = 0; i < (MF == 16 ? FM16 : 1); ++i)
+#pragma unroll
+        for (int j = 0; j < (MF == 16 ? FN16 : 1); ++j) acc16[i][j] = floatx4{};
     // LayerNorm consumer: the PPT consecutive lanes of tile row t / PPT load its 64-column
     // partials j = t % PPT, + PPT, ... (issued before the first K tiles, added after),
     // and thread t < NT the column sum of tile column t
@@ -524,6 +548,7 @@ void gemm_kernel(GemmArgs a) {
         __builtin_amdgcn_s_setprio(1);
         const f16* sA = smem + (kt % NS) * STAGE;
         const f16* sB = sA + MT * BKT;
+        if constexpr (MF == 32) {
         half8 af[2][FM], bf[2][FN];
         auto load_frags = [&](int ks, int slot) __attribute__((always_inline)) {
             const int pc = ((ks * 2 + hl) ^ sw) * 8;
@@ -554,6 +579,41 @@ void gemm_kernel(GemmArgs a) {
             }
             __builtin_amdgcn_sched_group_barrier(0x008, 2 * FM * FN, 0);
         }
+        } else {
+        // 16x16x32: row / column lane & 15, logical chunk 4 * ks + (lane >> 4); the
+        // fragment base rows are multiples of 16, so the swizzle depends on lane & 15 only
+        constexpr int KS16 = BKT / 32;
+        const int sw16 = lds_swizzle<BKT>(lane & 15);
+        half8 af[2][FM16], bf[2][FN16];
+        auto load_frags = [&](int ks, int slot) __attribute__((always_inline)) {
+            const int pc = ((ks * 4 + (lane >> 4)) ^ sw16) * 8;
+#pragma unroll
+            for (int i = 0; i < FM16; ++i)
+                af[slot][i] = *(const half8*)(sA + (wm * TMW + i * 16 + (lane & 15)) * BKT + pc);
+#pragma unroll
+            for (int j = 0; j < FN16; ++j)
+                bf[slot][j] = *(const half8*)(sB + (wn * TNW + j * 16 + (lane & 15)) * BKT + pc);
+        };
+        load_frags(0, 0);
+#pragma unroll
+        for (int ks = 0; ks < KS16; ++ks) {
+            if (ks + 1 < KS16) load_frags(ks + 1, (ks + 1) & 1);
+#pragma unroll
+            for (int i = 0; i < FM16; ++i)
+#pragma unroll
+                for (int j = 0; j < FN16; ++j)
+                    acc16[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[ks & 1][i], bf[ks & 1][j], acc16[i][j], 0, 0, 0);
+        }
+        if (KS16 >= 2) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 2 * (FM16 + FN16), 0);  // DS reads
+#pragma unroll
+            for (int ks = 0; ks < KS16 - 2; ++ks) {
+                __builtin_amdgcn_sched_group_barrier(0x008, FM16 * FN16, 0);  // MFMAs
+                __builtin_amdgcn_sched_group_barrier(0x100, FM16 + FN16, 0);  // DS reads
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 2 * FM16 * FN16, 0);
+        }
+        }
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         __builtin_amdgcn_s_setprio(0);
     }
@@ -577,6 +637,7 @@ void gemm_kernel(GemmArgs a) {
     if (a.partial && !a.fixup) {
         // split K, reduce kernel: fp32 partial [split][M][N]
         float* P = a.partial + (int64_t)blockIdx.z * a.M * a.N;
+        if constexpr (MF == 32) {
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -589,6 +650,20 @@ void gemm_kernel(GemmArgs a) {
                     if (m < a.M) P[(int64_t)m * a.N + n] = acc[i][j][e];
                 }
             }
+        } else {
+#pragma unroll
+        for (int i = 0; i < FM16; ++i)
+#pragma unroll
+            for (int j = 0; j < FN16; ++j) {
+                const int n = n0 + wn * TNW + j * 16 + (lane & 15);
+                if (n >= a.N) continue;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int m = m0 + wm * TMW + i * 16 + 4 * (lane >> 4) + e;
+                    if (m < a.M) P[(int64_t)m * a.N + n] = acc16[i][j][e];
+                }
+            }
+        }
         return;
     }
     if (a.partial) {
@@ -616,18 +691,33 @@ void gemm_kernel(GemmArgs a) {
         typedef float f32x4 __attribute__((ext_vector_type(4)));
         const __amdgpu_buffer_rsrc_t rsP = __builtin_amdgcn_make_buffer_rsrc(
             (void*)(a.partial + (int64_t)bid * a.splits * SLOT), (short)0, a.splits * SLOT * 4, 0x00020000);
-        const uint32_t vo_w = (uint32_t)((wave * FM * FN * 4 * 64 + lane) * 16);
+        // the lane's accumulators as QPL float4 quads: quad (i * FN + j) * 4 + q is elements
+        // 4q .. 4q+3 of the 32x32 fragment (i, j), or quad i * FN16 + j the 16x16 fragment
+        constexpr int QPL = MF == 32 ? FM * FN * 4 : FM16 * FN16;
+        auto get_quad = [&](int qi) __attribute__((always_inline)) -> f32x4 {
+            if constexpr (MF == 32) {
+                const int i = qi / (FN * 4), j = (qi / 4) % FN, q = qi % 4;
+                return f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+            } else {
+                const floatx4 v = acc16[qi / FN16][qi % FN16];
+                return f32x4{v[0], v[1], v[2], v[3]};
+            }
+        };
+        auto add_quad = [&](int qi, f32x4 v) __attribute__((always_inline)) {
+            if constexpr (MF == 32) {
+                const int i = qi / (FN * 4), j = (qi / 4) % FN, q = qi % 4;
 #pragma unroll
-        for (int i = 0; i < FM; ++i)
+                for (int e = 0; e < 4; ++e) acc[i][j][4 * q + e] += v[e];
+            } else {
 #pragma unroll
-            for (int j = 0; j < FN; ++j)
+                for (int e = 0; e < 4; ++e) acc16[qi / FN16][qi % FN16][e] += v[e];
+            }
+        };
+        const uint32_t vo_w = (uint32_t)((wave * QPL * 64 + lane) * 16);
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const f32x4 v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
-                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rsP,
-                                                           vo_w + ((i * FN + j) * 4 + q) * 1024,
-                                                           blockIdx.z * SLOT * 4, CPOL_SC1);
-                }
+        for (int qi = 0; qi < QPL; ++qi)
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, get_quad(qi)), rsP, vo_w + qi * 1024,
+                                                   blockIdx.z * SLOT * 4, CPOL_SC1);
         wait_vmcnt_lgkm0<0>();  // this wave's slot stores are complete
         __syncthreads();        // ... for every wave; no wave still reads the ring
         int* const flag = (int*)smem;
@@ -644,36 +734,29 @@ void gemm_kernel(GemmArgs a) {
         // the result does not depend on which block arrived last.  Slots go in rounds
         // of SPR, every load of a round issued before any is added (slot indices
         // clamped, repeats not added).
-        constexpr int SPR = FM * FN >= 4 ? 1 : 4 / (FM * FN);
+        constexpr int SPR = QPL >= 16 ? 1 : (QPL >= 8 ? 2 : 4);
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
             for (int j = 0; j < FN; ++j) acc[i][j] = floatx16{};
+#pragma unroll
+        for (int i = 0; i < (MF == 16 ? FM16 : 1); ++i)
+#pragma unroll
+            for (int j = 0; j < (MF == 16 ? FN16 : 1); ++j) acc16[i][j] = floatx4{};
         for (int z0 = 0; z0 < a.splits; z0 += SPR) {
-            f32x4 pv[SPR][FM][FN][4];
+            f32x4 pv[SPR][QPL];
 #pragma unroll
             for (int u = 0; u < SPR; ++u) {
                 const int so = min(z0 + u, a.splits - 1) * SLOT * 4;
 #pragma unroll
-                for (int i = 0; i < FM; ++i)
-#pragma unroll
-                    for (int j = 0; j < FN; ++j)
-#pragma unroll
-                        for (int q = 0; q < 4; ++q)
-                            pv[u][i][j][q] = __builtin_bit_cast(
-                                f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsP, vo_w + ((i * FN + j) * 4 + q) * 1024, so, CPOL_SC1));
+                for (int qi = 0; qi < QPL; ++qi)
+                    pv[u][qi] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsP, vo_w + qi * 1024, so, CPOL_SC1));
             }
 #pragma unroll
             for (int u = 0; u < SPR; ++u) {
                 const bool use = z0 + u < a.splits;
 #pragma unroll
-                for (int i = 0; i < FM; ++i)
-#pragma unroll
-                    for (int j = 0; j < FN; ++j)
-#pragma unroll
-                        for (int q = 0; q < 4; ++q)
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) acc[i][j][4 * q + e] += use ? pv[u][i][j][q][e] : 0.f;
+                for (int qi = 0; qi < QPL; ++qi) add_quad(qi, use ? pv[u][qi] : f32x4{0.f, 0.f, 0.f, 0.f});
             }
         }
     }
@@ -740,6 +823,7 @@ void gemm_kernel(GemmArgs a) {
             if (tid % PPT == 0) ln_rt[tid / PPT] = ln_rs;
             if (tid < NT) ln_cs[tid] = ln_cs_t;
         }
+        if constexpr (MF == 32) {
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
@@ -747,6 +831,17 @@ void gemm_kernel(GemmArgs a) {
                 const int r = wm * 32 + (e >> 2) * 8 + rq + (e & 3);
                 Cs[r * CST + wn * TNW + j * 32 + col_l] = acc[ip][j][e];
             }
+        } else {
+#pragma unroll
+        for (int i = 0; i < FM16; ++i)
+#pragma unroll
+            for (int j = 0; j < FN16; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int r = wm * 32 + i * 16 + 4 * (lane >> 4) + e;
+                    Cs[r * CST + wn * TNW + j * 16 + (lane & 15)] = acc16[i][j][e];
+                }
+        }
         __syncthreads();
         // staged row s <-> tile row (s / 32) * TMW + ip * 32 + s % 32
         if (narrow) {
@@ -761,7 +856,7 @@ void gemm_kernel(GemmArgs a) {
             }
             continue;
         }
-        if (n >= a.N) continue;
+        if (n >= a.N || !ep_on) continue;
         if (!PRE) load_res(ip);
 #pragma unroll
         for (int k = 0; k < MAXR; ++k) {
@@ -942,24 +1037,42 @@ struct Cfg {
     int mt, nt, per_cu;   // tile, resident blocks per CU (LDS-limited)
     double rate1, rate2;  // measured MFMA FLOP/s of one CU running 1 / 2 such blocks
     double t_fix;         // per-block prologue + epilogue time
+    int spr;              // split slots per modelled round of the summing block's tail
+    double conv_f;        // rate factor with the implicit-conv A (the tap gather)
 };
 // 0: 256x128, 8 waves of 64x64, BK 64, 2-stage ring (96 KB: one block per CU)
 // 1: 128x128, 8 waves of 64x32, BK 64, 2-stage ring (64 KB: two per CU, 4 waves per SIMD)
 // 2: 128x64,  8 waves of 32x32, BK 64, 3-stage ring (72 KB: two per CU, 4 waves per SIMD)
+// 3: 64x160,  4 waves of 32x80 (16x16x32 MFMAs), BK 64, 2-stage ring (56 KB: two per CU)
 // Rates and fixed costs from dense GEMMs that give every CU one or two blocks, at
 // K = 512 and 4096 (the difference gives the rate, the rest the fixed cost).  The
 // 128x128 two-block rate is set above that fit (3.54): the 64x64 convs over the up
 // path's concatenated inputs run two splits as co-resident pairs faster than it
 // predicts (640 -> 320: 56.6 us with 2 splits against 62.4 with 4), and whole forwards
 // compared in one call take 5.09 against 5.10 ms (B=2 64x64), 9.69 against 9.78 (96x96)
-// and 21.45 against 21.45 (B=16).
-const Cfg kCfgs[3] = {{256, 128, 1, 3.5e12, 3.5e12, 4.5e-6},
-                      {128, 128, 2, 2.76e12, 3.9e12, 3.0e-6},
-                      {128, 64, 2, 2.23e12, 3.03e12, 2.5e-6}};
+// and 21.45 against 21.45 (B=16).  The implicit-conv A (a tap gather per row) costs the
+// 64-column tile about 20% of its rate.
+// The 64x160 tile covers N = 320 with no padded column and M = 8192 with 256 tiles, so it
+// fills the chip where 128-row tiles leave a quarter of the CUs idle, but its own rate is
+// lower (4 waves, 46 FLOP per operand byte against 64): its parameters are fitted to 18
+// UNet GEMMs timed with both tiles in one forward (B=2 and 16, 64x64 latents), on which
+// they pick the faster tile every time.  It wins on the 64x64 level's convs at B=2
+// (M = 8192, N = 320: 39.4 against 42.3 us at K = 2880, 79.1 against 94.3 at K = 8640)
+// and loses at larger M (B=16, M = 65536: 192.6 against 178.3 us).
+constexpr int kNumCfg = 4;
+// The tail model counts one slot per round for the 128-row tiles and two for the others
+// (their kernels load 1, 2, 4 and 2 slots per round): moving the 128x128 tile to its
+// kernel's 2 sends the 64x64 and 48x48 levels' concat convs from the reduce launch to the
+// in-kernel sum and changed them by -10% to +15% each, no gain over a forward.
+const Cfg kCfgs[kNumCfg] = {{256, 128, 1, 3.5e12, 3.5e12, 4.5e-6, 1, 1.0},
+                            {128, 128, 2, 2.76e12, 3.9e12, 3.0e-6, 1, 1.0},
+                            {128, 64, 2, 2.23e12, 3.03e12, 2.5e-6, 2, 0.8},
+                            {64, 160, 2, 2.0e12, 3.4e12, 6.0e-6, 2, 0.9}};
 // full kernel names (tile configuration, then the A mode: 0 dense, 1 implicit conv)
-const char* const kNames[3][2] = {{"gemm_kernel<256,128,4,2,64,2,0>", "gemm_kernel<256,128,4,2,64,2,1>"},
-                                  {"gemm_kernel<128,128,2,4,64,2,0>", "gemm_kernel<128,128,2,4,64,2,1>"},
-                                  {"gemm_kernel<128,64,4,2,64,3,0>", "gemm_kernel<128,64,4,2,64,3,1>"}};
+const char* const kNames[kNumCfg][2] = {{"gemm_kernel<256,128,4,2,64,2,0>", "gemm_kernel<256,128,4,2,64,2,1>"},
+                                        {"gemm_kernel<128,128,2,4,64,2,0>", "gemm_kernel<128,128,2,4,64,2,1>"},
+                                        {"gemm_kernel<128,64,4,2,64,3,0>", "gemm_kernel<128,64,4,2,64,3,1>"},
+                                        {"gemm_kernel<64,160,2,2,64,2,0,16>", "gemm_kernel<64,160,2,2,64,2,1,16>"}};
 
 int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
@@ -968,10 +1081,6 @@ int ceil_div(int a, int b) { return (a + b - 1) / b; }
 // modelled cost of its tail.
 constexpr int kMaxSplitTiles = 16384;
 constexpr size_t kCounterBytes = kMaxSplitTiles * sizeof(unsigned);
-int fix_slots_per_round(int mt, int nt) {
-    const int f = (mt / 64) * (nt / 64);  // 32x32 fragments per wave (8 waves)
-    return f >= 4 ? 1 : 4 / f;
-}
 constexpr double kFixBase = 1.0e-6, kFixRound = 0.9e-6;
 
 // The epilogue keeps output statistics for two images per tile: the MT rows of a tile
@@ -988,9 +1097,15 @@ void plan(const GemmArgs& a, int& ci, int& splits, int& kps, bool& fix) {
     const int nkt = ceil_div(a.K, 64);
     double best = 1e30;
     ci = 1; splits = 1; kps = nkt * 64; fix = false;
-    for (int c = 0; c < 3; ++c) {
+    for (int c = 0; c < kNumCfg; ++c) {
         const Cfg& g = kCfgs[c];
-        if (a.geglu && g.nt < 128) continue;  // GEGLU pairs 32-column blocks within a 64-wide wave tile
+        if (a.geglu && g.nt % 128) continue;  // GEGLU pairs 32-column blocks within a 64-wide wave tile
+        // LayerNorm row partials: one per 64 columns, summed by 8 consecutive lanes
+        if (a.row_part && g.nt % 64) continue;
+        // the LayerNorm consumer's epilogue runs 5-8% slower in the 4-wave 64x160 tile than
+        // the 128x128 tile at K = 1280 (M = 1152, N = 3840: 27.8 against 25.7 us), which
+        // the model does not see
+        if (a.ln_part && g.mt == 64) continue;
         if (a.stats && !stats_tile_ok(g.mt, a.stats_hw)) continue;
         const int tiles = ceil_div(a.M, g.mt) * ceil_div(a.N, g.nt);
         static const int cand[] = {1, 2, 3, 4, 6, 8, 12, 16, 24, 32};
@@ -1002,9 +1117,7 @@ void plan(const GemmArgs& a, int& ci, int& splits, int& kps, bool& fix) {
             const long load = (blocks + 255) / 256;  // blocks on the busiest CU
             const double w = 2.0 * g.mt * g.nt * kt_per * 64.0;
             const long pairs = g.per_cu >= 2 ? load / 2 : 0, singles = load - 2 * pairs;
-            // implicit-conv A (a tap gather per 128 rows) costs the 64-column tile a
-            // larger share of its time than a dense A: about 20% of its rate
-            const double cf = (a.amode == A_CONV3 && g.nt < 128) ? 0.8 : 1.0;
+            const double cf = a.amode == A_CONV3 ? g.conv_f : 1.0;
             double t = pairs * (2.0 * w / (g.rate2 * cf) + g.t_fix) + singles * (w / (g.rate1 * cf) + g.t_fix);
             // a split adds the partial round trip, and either the reduce launch (about
             // 5.5 us, 2 us more with statistics) or the serial tail of each tile's last
@@ -1014,7 +1127,7 @@ void plan(const GemmArgs& a, int& ci, int& splits, int& kps, bool& fix) {
                 const double part = (double)se * a.M * a.N * 8.0 / 20.0e12;
                 // (with output statistics only the in-kernel sum: the reduce keeps none)
                 const double t_red = (a.stats || a.row_part || a.ln_part) ? 1e30 : part + 5.5e-6;
-                const int rounds = ceil_div(se, fix_slots_per_round(g.mt, g.nt));
+                const int rounds = ceil_div(se, g.spr);
                 const double t_fix = tiles <= kMaxSplitTiles ? part + kFixBase + kFixRound * rounds : 1e30;
                 fx = t_fix < t_red;
                 t += fx ? t_fix : t_red;
@@ -1052,7 +1165,8 @@ template <int AM>
 static void launch_cfg(int ci, dim3 grid, const GemmArgs& a, hipStream_t s) {
     if (ci == 0) SDU_LAUNCH((gemm_kernel<256, 128, 4, 2, 64, 2, AM>), grid, dim3(512), 0, s, a);
     else if (ci == 1) SDU_LAUNCH((gemm_kernel<128, 128, 2, 4, 64, 2, AM>), grid, dim3(512), 0, s, a);
-    else SDU_LAUNCH((gemm_kernel<128, 64, 4, 2, 64, 3, AM>), grid, dim3(512), 0, s, a);
+    else if (ci == 2) SDU_LAUNCH((gemm_kernel<128, 64, 4, 2, 64, 3, AM>), grid, dim3(512), 0, s, a);
+    else SDU_LAUNCH((gemm_kernel<64, 160, 2, 2, 64, 2, AM, 16>), grid, dim3(256), 0, s, a);
 }
 
 hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s) {
