@@ -496,7 +496,7 @@ static void launch_cfg(const AttnArgs& a, hipStream_t s) {
         // d40 at 4096 tokens, B=2, 0.44 ms per forward against 0.46 with 64-key tiles;
         // on larger grids they lose (0.24 ms more at 9216 tokens, 0.31 ms at B=16)
         const bool kt128 = KS == 3 && nw == 4 && (long)grid.x * bh <= 512;
-        snprintf(name, sizeof name, "attn_kernel<%d,%d,%d,%d%s>", KS, MTD, nw, (int)LSUM, kt128 ? ",128" : "");
+        snprintf(name, sizeof name, "attn_kernel<%d,%d,%d,%d,%d>", KS, MTD, nw, (int)LSUM, kt128 ? 128 : 64);
         launch_timed(name, flops, bytes, [&] {
             if (nw == 8) SDU_LAUNCH((attn_kernel<KS, MTD, 8, LSUM>), grid, dim3(512), 0, s, a);
             else if (KS == 3 && kt128) SDU_LAUNCH((attn_kernel<KS, MTD, 4, LSUM, (KS == 3 ? 128 : 64)>), grid, dim3(256), 0, s, a);

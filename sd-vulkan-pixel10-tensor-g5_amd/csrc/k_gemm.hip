@@ -1068,10 +1068,11 @@ const Cfg kCfgs[kNumCfg] = {{256, 128, 1, 3.5e12, 3.5e12, 4.5e-6, 1, 1.0},
                             {128, 128, 2, 2.76e12, 3.9e12, 3.0e-6, 1, 1.0},
                             {128, 64, 2, 2.23e12, 3.03e12, 2.5e-6, 2, 0.8},
                             {64, 160, 2, 2.0e12, 3.4e12, 6.0e-6, 2, 0.9}};
-// full kernel names (tile configuration, then the A mode: 0 dense, 1 implicit conv)
-const char* const kNames[kNumCfg][2] = {{"gemm_kernel<256,128,4,2,64,2,0>", "gemm_kernel<256,128,4,2,64,2,1>"},
-                                        {"gemm_kernel<128,128,2,4,64,2,0>", "gemm_kernel<128,128,2,4,64,2,1>"},
-                                        {"gemm_kernel<128,64,4,2,64,3,0>", "gemm_kernel<128,64,4,2,64,3,1>"},
+// full kernel names, as the instantiations (tile configuration, A mode: 0 dense, 1 implicit conv,
+// then the MFMA)
+const char* const kNames[kNumCfg][2] = {{"gemm_kernel<256,128,4,2,64,2,0,32>", "gemm_kernel<256,128,4,2,64,2,1,32>"},
+                                        {"gemm_kernel<128,128,2,4,64,2,0,32>", "gemm_kernel<128,128,2,4,64,2,1,32>"},
+                                        {"gemm_kernel<128,64,4,2,64,3,0,32>", "gemm_kernel<128,64,4,2,64,3,1,32>"},
                                         {"gemm_kernel<64,160,2,2,64,2,0,16>", "gemm_kernel<64,160,2,2,64,2,1,16>"}};
 
 int ceil_div(int a, int b) { return (a + b - 1) / b; }
