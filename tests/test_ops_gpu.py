@@ -125,6 +125,9 @@ def test_layernorm(op_engine, T, C):
     (96, 320, 640, 0, True, True, False, True),          # ragged M, fp32 out
     (64, 1280, 1280, 0, False, True, False, False),      # M = 64
     (33, 64, 128, 0, True, False, True, False),          # ragged M, GEGLU
+    # the 64x160 tile (16x16x32 MFMAs): ragged M with split K, and the 77-token cross K/V
+    (8000, 320, 2880, 0, True, True, False, False),
+    (154, 24960, 768, 0, False, False, False, False),
 ])
 def test_matmul(op_engine, M, N, K, K2, bias, res, geglu, f32):
     say(f"matmul M={M} N={N} K={K} K2={K2} bias={bias} res={res} geglu={geglu} f32={f32}")
@@ -199,6 +202,9 @@ def test_matmul_split_repeat(op_engine):
     (2, 16, 16, 1280, 1280, 3, 2, False, False, False),  # downsample to 8x8 (M = 128)
     (1, 8, 8, 640, 320, 3, 1, False, True, True),      # M = 64
     (1, 6, 10, 128, 96, 3, 1, False, False, True),     # ragged M = 60, Cin = 128
+    # the 64x160 tile (16x16x32 MFMAs) with split K: ragged M = 8100, non-square image
+    (1, 90, 90, 320, 320, 3, 1, False, True, True),
+    (2, 62, 66, 320, 320, 3, 1, False, False, False),
 ])
 def test_conv2d(op_engine, B, H, W, Ci, Co, k, stride, ups, temb, res):
     say(f"conv2d B={B} {H}x{W} {Ci}->{Co} k={k} s={stride} ups={ups} temb={temb} res={res}")
