@@ -128,6 +128,8 @@ def test_layernorm(op_engine, T, C):
     # the 64x160 tile (16x16x32 MFMAs): ragged M with split K, and the 77-token cross K/V
     (8000, 320, 2880, 0, True, True, False, False),
     (154, 24960, 768, 0, False, False, False, False),
+    (8192, 300, 2880, 0, True, False, False, True),  # N % 8 != 0: element-wise epilogue
+    (8000, 312, 2880, 0, True, True, False, False),  # last N tile partly outside N
 ])
 def test_matmul(op_engine, M, N, K, K2, bias, res, geglu, f32):
     say(f"matmul M={M} N={N} K={K} K2={K2} bias={bias} res={res} geglu={geglu} f32={f32}")
@@ -205,6 +207,7 @@ def test_matmul_split_repeat(op_engine):
     # the 64x160 tile (16x16x32 MFMAs) with split K: ragged M = 8100, non-square image
     (1, 90, 90, 320, 320, 3, 1, False, True, True),
     (2, 62, 66, 320, 320, 3, 1, False, False, False),
+    (1, 90, 90, 320, 312, 3, 1, False, True, True),    # last N tile partly outside N
 ])
 def test_conv2d(op_engine, B, H, W, Ci, Co, k, stride, ups, temb, res):
     say(f"conv2d B={B} {H}x{W} {Ci}->{Co} k={k} s={stride} ups={ups} temb={temb} res={res}")
