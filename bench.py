@@ -312,8 +312,16 @@ def main():
             e["gbs"] = round(v["bytes"] / (v["ms"] * 1e-3) / 1e9, 1)
             e["frac_hbm"] = round(e["gbs"] / PEAK_HBM_GBS, 4)
         per_kernel[k] = e
-    per_cat = {k: {"calls": v["calls"], "ms": round(v["ms"], 4)} for k, v in
-               sorted(cats.items(), key=lambda kv: -kv[1]["ms"])}
+    # per op category (all kernels of the op, e.g. every conv 3x3 GEMM tile shape and its
+    # split-K reduce): algorithmic FLOPs or bytes over the category's summed launch times
+    per_cat = {}
+    for k, v in sorted(cats.items(), key=lambda kv: -kv[1]["ms"]):
+        e = {"calls": v["calls"], "ms": round(v["ms"], 4)}
+        if v["flops"] > 0:
+            e["frac_mfma"] = round(v["flops"] / (v["ms"] * 1e-3) / 1e12 / PEAK_MFMA_TFLOPS, 4)
+        elif v["bytes"] > 0:
+            e["frac_hbm"] = round(v["bytes"] / (v["ms"] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)
+        per_cat[k] = e
 
     # the other single-GPU shapes: B=2 96x96 (9216-token attention) and B=16 64x64
     extra = {}
