@@ -130,6 +130,10 @@ def test_layernorm(op_engine, T, C):
     (154, 24960, 768, 0, False, False, False, False),
     (8192, 300, 2880, 0, True, False, False, True),  # N % 8 != 0: element-wise epilogue
     (8000, 312, 2880, 0, True, True, False, False),  # last N tile partly outside N
+    # small dense GEMMs of the transformer blocks: ragged M, fp32 out, two K sources
+    (8000, 320, 320, 0, True, True, False, False),
+    (2048, 640, 640, 0, True, False, False, True),
+    (8192, 320, 1600, 1280, True, True, False, False),
 ])
 def test_matmul(op_engine, M, N, K, K2, bias, res, geglu, f32):
     say(f"matmul M={M} N={N} K={K} K2={K2} bias={bias} res={res} geglu={geglu} f32={f32}")
