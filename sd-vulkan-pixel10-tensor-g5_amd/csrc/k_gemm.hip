@@ -1055,10 +1055,11 @@ struct Cfg {
 // The 64x160 tile covers N = 320 with no padded column and M = 8192 with 256 tiles, so it
 // fills the chip where 128-row tiles leave a quarter of the CUs idle, but its own rate is
 // lower (4 waves, 46 FLOP per operand byte against 64): its parameters are fitted to 18
-// UNet GEMMs timed with both tiles in one forward (B=2 and 16, 64x64 latents), on which
-// they pick the faster tile every time.  It wins on the 64x64 level's convs at B=2
-// (M = 8192, N = 320: 39.4 against 42.3 us at K = 2880, 79.1 against 94.3 at K = 8640)
-// and loses at larger M (B=16, M = 65536: 192.6 against 178.3 us).
+// UNet GEMMs timed with both tiles in one forward (B=2 and 16, 64x64 latents).  In whole
+// forwards the planner then takes it for the 64x64 level's convs at B=2 (M = 8192,
+// N = 320: 38.5 against 41.8 us at K = 2880, 83.4 against 93.0 at K = 8640), the 77-token
+// cross K/V GEMM (21.2 against 24.6 us) and two B=16 feed-forward outputs, each faster
+// than before; it loses at larger M (B=16 conv, M = 65536: 192.6 against 178.3 us).
 constexpr int kNumCfg = 4;
 // The tail model counts one slot per round for the 128-row tiles and two for the others
 // (their kernels load 1, 2, 4 and 2 slots per round): moving the 128x128 tile to its
