@@ -14,7 +14,7 @@
 // Both passes accept a second source concatenated along channels (the up-path
 // skip concat, vk_engine.cpp:678-688), so the concat is never materialised.
 // When one (image, group) slab is small (HW * C/G <= 32K elements: the 32x32 and
-// smaller levels of the 64x64 UNet) and fits the registers of a 1024-thread block,
+// smaller levels of the 64x64 UNet) and fits the registers of a 512-thread block,
 // a single kernel does it all: the slab is loaded once, mean and variance are
 // reduced exactly in two passes over the registers, and the normalised values are
 // stored -- one launch, one read and one write of the tensor.
@@ -261,7 +261,10 @@ __global__ void zero_kernel(uint4* p, int64_t n16) {
 
 // ----------------------------------------------------------------- single-pass GroupNorm
 
-static constexpr int GNF_THREADS = 1024;
+// 512 threads: the 8x8 - 32x32 slabs (2.5K - 20K elements) leave most of a 1024-thread
+// block idle through its block reductions; per forward the GroupNorms took 418 against
+// 434 us at B=2 64x64 and 898 against 976 us at B=16 (256 threads: 467 / 921 us).
+static constexpr int GNF_THREADS = 512;
 
 // Sums over the block of two floats per thread, in fp64 across waves; every thread
 // gets the results.
