@@ -119,7 +119,9 @@ __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)
 // CST = false: acc holds the per-group sums [B][G][2] of gn_stats_kernel.
 // CST = true: acc and st2 hold per-channel sums [B][C1][2] and [B][C2][2] written by
 // the GEMM epilogues that produced x and x2; 8 threads add up each group's channels.
-static constexpr int GNA_VPT = 4;
+// 2 vectors per thread and chunk: the apply passes of B=2 took 127 against 136 us per 64x64
+// forward and 309 against 318 us per 96x96 forward with 4 (B=16 434 against 431 us)
+static constexpr int GNA_VPT = 2;
 static constexpr int GNA_VEC = GN_THREADS * GNA_VPT;
 
 // Branch-free loads of one chunk (index clamped to the last vector of the image).
