@@ -263,6 +263,20 @@ int sdu_conv2d(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* w, const sdu
                const sdu_tensor* temb, const sdu_tensor* residual, sdu_tensor* y, int B, int H,
                int W, int Ci, int Co, int ksize, int stride, int upsample, int flags);
 
+/* A 3x3 conv (stride 1, no upsample; as sdu_conv2d with ksize 3) followed by the
+ * groupnorm / groupnorm_silu of its output (vk_engine.cpp:626-631, the resnet's conv1 ->
+ * norm2 step), in the engine's fused form: the conv's epilogue adds the per-channel sums
+ * and sums of squares of its stored fp16 output (fp32 per tile, fp64 across tiles) and the
+ * GroupNorm forms each group's mean and variance from them.  No separate counterpart in
+ * the reference's op list: it exposes the path the UNet takes for its 64x64-level
+ * GroupNorms to op-level callers and tests.  y NHWC [B,H,W,Co] (the conv output) and
+ * gn_y NHWC [B,H,W,Co] (its GroupNorm); gamma/beta fp16 [Co]; H*W >= 64, Co % 8 == 0,
+ * groups <= 32 and Co % groups == 0. */
+int sdu_conv2d_groupnorm(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* w, const sdu_tensor* bias,
+                         const sdu_tensor* temb, const sdu_tensor* residual, sdu_tensor* y,
+                         const sdu_tensor* gamma, const sdu_tensor* beta, sdu_tensor* gn_y, int B, int H,
+                         int W, int Ci, int Co, int groups, float eps, int silu);
+
 /* ATTN / ATTN_BIG (vk_engine.cpp:655, :663): per image b and head h,
  * o = softmax(q k^T * scale) v.  q rows b*Sq+i, k/v rows b*Sk+j, head h at column
  * h*d; ldq/ldk/ldv/ldo are row strides in elements.  d in {8,...,160}, d % 8 == 0. */

@@ -42,7 +42,7 @@ EXPORTS = [
     "sdu_forward_device", "sdu_denoise_lcm_device", "sdu_denoise_lcm_ex", "sdu_selftest", "sdu_selftest_ex", "sdu_time_proj", "sdu_profile",
     "sdu_tensor_alloc", "sdu_tensor_free", "sdu_tensor_upload", "sdu_tensor_download",
     "sdu_tensor_device_ptr", "sdu_tensor_bytes", "sdu_groupnorm", "sdu_groupnorm_noalloc", "sdu_layernorm", "sdu_matmul",
-    "sdu_conv2d", "sdu_attention", "sdu_attention_ex", "sdu_geglu", "sdu_silu", "sdu_add", "sdu_add_bias",
+    "sdu_conv2d", "sdu_conv2d_groupnorm", "sdu_attention", "sdu_attention_ex", "sdu_geglu", "sdu_silu", "sdu_add", "sdu_add_bias",
     "sdu_lcm_step", "sdu_taesd_init", "sdu_taesd_decode", "sdu_taesd_decode_device", "sdu_clip_init",
     "sdu_clip_encode", "sdu_clip_encode_device", "sdu_generate", "sdu_calibrate",
 ]
@@ -116,6 +116,7 @@ def load(path: str = LIB_PATH):
         "sdu_layernorm": ([P, P, P, P, P, I, I, F], I),
         "sdu_matmul": ([P, P, P, P, P, P, P, I, I, I, I, I], I),
         "sdu_conv2d": ([P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I], I),
+        "sdu_conv2d_groupnorm": ([P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, F, I], I),
         "sdu_attention": ([P, P, P, P, P, I, I, I, I, I, I, I, I, I, F], I),
         "sdu_attention_ex": ([P, P, P, P, P, I, I, I, I, I, I, I, I, I, F, I], I),
         "sdu_taesd_init": ([P, ctypes.c_char_p, ctypes.c_uint64, I], I),
@@ -345,6 +346,14 @@ class Engine:
         self._check(load().sdu_conv2d(self.h, x.h, w.h, bias.h if bias else None,
                                       temb.h if temb else None, residual.h if residual else None,
                                       y.h, B, H, W, Ci, Co, ksize, stride, int(upsample), flags))
+
+    def conv2d_groupnorm(self, x, w, y, gamma, beta, gn_y, B, H, W, Ci, Co, bias=None, temb=None,
+                         residual=None, groups=32, eps=1e-5, silu=True):
+        """3x3 conv whose epilogue keeps the GroupNorm statistics, then GroupNorm(+SiLU)."""
+        self._check(load().sdu_conv2d_groupnorm(self.h, x.h, w.h, bias.h if bias else None,
+                                                temb.h if temb else None, residual.h if residual else None,
+                                                y.h, gamma.h, beta.h, gn_y.h, B, H, W, Ci, Co, groups, eps,
+                                                int(silu)))
 
     def attention(self, q, k, v, o, B, heads, Sq, Sk, d, ldq, ldk, ldv, ldo, scale):
         self._check(load().sdu_attention(self.h, q.h, k.h, v.h, o.h, B, heads, Sq, Sk, d, ldq, ldk,

@@ -85,6 +85,52 @@ def test_groupnorm_large_mean(op_engine, B, H, W, C, silu):
     assert np.abs(got - ref).max() < 2e-2
 
 
+@pytest.mark.parametrize("B,H,W,Ci,Co,mean,temb,res,silu", [
+    (2, 64, 64, 320, 320, 0.0, True, False, True),    # resnet conv1 -> norm2 at 64x64
+    (2, 64, 64, 320, 320, 100.0, False, False, True),  # output mean 100x its spread
+    (3, 40, 40, 64, 640, 30.0, False, True, False),    # 1600-pixel images: tiles straddle two
+    (1, 8, 8, 128, 320, 50.0, True, False, True),      # 64-pixel images
+])
+def test_conv_groupnorm_epilogue_stats(op_engine, B, H, W, Ci, Co, mean, temb, res, silu):
+    """The UNet's 64x64-level GroupNorm path: per-channel sums and sums of squares of the
+    conv's stored fp16 output, kept by the GEMM epilogue (fp32 per tile, fp64 across tiles),
+    then the GroupNorm from them.  The conv output is checked against the fp32 conv; the
+    GroupNorm against an fp64 GroupNorm of the same fp16 conv output, so the check isolates
+    the statistics.  A large output mean is the case where E[x^2] - mean^2 cancels."""
+    say(f"conv+groupnorm B={B} {H}x{W} {Ci}->{Co} mean={mean} temb={temb} res={res} silu={silu}")
+    e = op_engine
+    HW = H * W
+    x = r16((B, H, W, Ci), 31)
+    w = r16((Co, Ci, 3, 3), 32, 1.0 / math.sqrt(Ci * 9))
+    bb = r16((Co,), 33, 0.5, mean)
+    tp = np.random.default_rng(34).standard_normal(Co).astype(np.float32)
+    rr = r16((B, H, W, Co), 35)
+    g = r16((Co,), 36, 0.3, 1.0)
+    b = r16((Co,), 37, 0.3)
+    tx = e.upload(x.astype(np.float16))
+    tw = e.upload(w.transpose(0, 2, 3, 1).astype(np.float16))
+    tb = e.upload(bb.astype(np.float16))
+    tt = e.upload(tp) if temb else None
+    tr = e.upload(rr.astype(np.float16)) if res else None
+    tg, tbeta = e.upload(g.astype(np.float16)), e.upload(b.astype(np.float16))
+    ty, tgn = e.tensor((B, H, W, Co)), e.tensor((B, H, W, Co))
+    e.conv2d_groupnorm(tx, tw, ty, tg, tbeta, tgn, B, H, W, Ci, Co, bias=tb, temb=tt, residual=tr, silu=silu)
+    ref = U.conv2d(t(x.transpose(0, 3, 1, 2)), t(w), t(bb), stride=1, pad=1)
+    if temb:
+        ref = ref + t(tp)[None, :, None, None]
+    ref = ref.numpy().transpose(0, 2, 3, 1)
+    if res:
+        ref = ref + rr
+    y = ty.numpy().astype(np.float32)
+    assert rel_err_l1(y, ref) < 1e-3
+    yn = t(y.reshape(B, HW, Co).transpose(0, 2, 1).reshape(B, Co, H, W)).double()
+    gref = U.group_norm(yn, t(g).double(), t(b).double(), act_silu=silu).float().numpy()
+    gref = gref.reshape(B, Co, HW).transpose(0, 2, 1).reshape(B, H, W, Co)
+    got = tgn.numpy().astype(np.float32)
+    assert rel_err_l1(got, gref) < 1e-3
+    assert np.abs(got - gref).max() < 2e-2
+
+
 # ------------------------------------------------------------------ LayerNorm
 
 
