@@ -270,8 +270,9 @@ int sdu_conv2d(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* w, const sdu
  * GroupNorm forms each group's mean and variance from them.  No separate counterpart in
  * the reference's op list: it exposes the path the UNet takes for its 64x64-level
  * GroupNorms to op-level callers and tests.  y NHWC [B,H,W,Co] (the conv output) and
- * gn_y NHWC [B,H,W,Co] (its GroupNorm); gamma/beta fp16 [Co]; H*W >= 64, Co % 8 == 0,
- * groups <= 32 and Co % groups == 0. */
+ * gn_y NHWC [B,H,W,Co] (its GroupNorm); gamma/beta fp16 [Co]; H*W = 64 or >= 128 (a
+ * 128-row output tile spans at most two images), Co % 8 == 0, groups <= 32 and
+ * Co % groups == 0; other shapes are SDU_ERR_ARG. */
 int sdu_conv2d_groupnorm(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* w, const sdu_tensor* bias,
                          const sdu_tensor* temb, const sdu_tensor* residual, sdu_tensor* y,
                          const sdu_tensor* gamma, const sdu_tensor* beta, sdu_tensor* gn_y, int B, int H,
