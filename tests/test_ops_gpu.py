@@ -405,6 +405,11 @@ def test_op_argument_errors(op_engine):
         e.attention(a, a, a, a, 1, 1, 4, 4, 168, 168, 168, 168, 168, 1.0)  # d > 160
     with pytest.raises(sdu.SduError):
         e.groupnorm(a, a, a, a, 1, 16, 12, 0)  # C not a multiple of 8
+    big = e.tensor((1, 10, 10, 64))
+    with pytest.raises(sdu.SduError) as ex:  # 100-pixel images: a 128-row tile spans three
+        e.conv2d_groupnorm(big, e.tensor((64, 3, 3, 64)), big, e.tensor((64,)), e.tensor((64,)), big,
+                           1, 10, 10, 64, 64)
+    assert ex.value.code == sdu.SDU_ERR_ARG
     with pytest.raises(sdu.SduError):
         e.forward(np.zeros((1, 4, 64, 64), np.float32), np.zeros(320, np.float32),
                   np.zeros((1, 77, 768), np.float32))  # context has no UNet weights
