@@ -249,7 +249,9 @@ int sdu_layernorm(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* gamma, co
 /* matmul (vk_engine.cpp:612-613) with fused epilogue:
  * y[M,N] = a[M,K] . w[N,K]^T (+ bias[N]) (+ residual[M,N]).
  * a2 (may be NULL) supplies columns [K1, K) of a (a = [a | a2], K1 = K - K2):
- * the 1x1 shortcut over a concatenated input. */
+ * the 1x1 shortcut over a concatenated input.  y must not overlap a, a2, w or bias;
+ * residual may be y itself (an in-place add) but must not otherwise overlap it
+ * (SDU_ERR_ARG). */
 int sdu_matmul(sdu_ctx* ctx, const sdu_tensor* a, const sdu_tensor* a2, const sdu_tensor* w,
                const sdu_tensor* bias, const sdu_tensor* residual, sdu_tensor* y,
                int M, int N, int K, int K2, int flags);
@@ -258,7 +260,8 @@ int sdu_matmul(sdu_ctx* ctx, const sdu_tensor* a, const sdu_tensor* a2, const sd
  * (k = 1 or 3, pad k/2), stride 1 or 2, optional nearest-2x upsample of the input
  * (upsample(), vk_engine.cpp:693-697).  y NHWC [B,Ho,Wo,Co] (+bias[Co])
  * (+ temb[Co] float32 broadcast, the resnet's time projection, :630)
- * (+ residual NHWC [B,Ho,Wo,Co]). */
+ * (+ residual NHWC [B,Ho,Wo,Co]).  y must not overlap x, w, bias or temb; residual
+ * may be y itself but must not otherwise overlap it (SDU_ERR_ARG). */
 int sdu_conv2d(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* w, const sdu_tensor* bias,
                const sdu_tensor* temb, const sdu_tensor* residual, sdu_tensor* y, int B, int H,
                int W, int Ci, int Co, int ksize, int stride, int upsample, int flags);
@@ -272,7 +275,9 @@ int sdu_conv2d(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* w, const sdu
  * GroupNorms to op-level callers and tests.  y NHWC [B,H,W,Co] (the conv output) and
  * gn_y NHWC [B,H,W,Co] (its GroupNorm); gamma/beta fp16 [Co]; H*W = 64 or >= 128 (a
  * 128-row output tile spans at most two images), Co % 8 == 0, groups <= 32 and
- * Co % groups == 0; other shapes are SDU_ERR_ARG. */
+ * Co % groups == 0; other shapes are SDU_ERR_ARG.  y follows sdu_conv2d's overlap
+ * rules and must not overlap gamma or beta either; gn_y may be y itself or any input of
+ * the conv, but not gamma, beta or a shifted view of y (SDU_ERR_ARG). */
 int sdu_conv2d_groupnorm(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* w, const sdu_tensor* bias,
                          const sdu_tensor* temb, const sdu_tensor* residual, sdu_tensor* y,
                          const sdu_tensor* gamma, const sdu_tensor* beta, sdu_tensor* gn_y, int B, int H,

@@ -3,6 +3,7 @@
 #include "engine.h"
 
 #include <cmath>
+#include <cstdint>
 #include <cstdio>
 #include <cstring>
 #include <fstream>
@@ -43,6 +44,25 @@ const void* dptr(const sdu_tensor* t) { return t ? t->t.ptr : nullptr; }
 void* dptr(sdu_tensor* t) { return t ? t->t.ptr : nullptr; }
 
 bool fits(const sdu_tensor* t, size_t bytes) { return t && t->t.bytes >= bytes; }
+
+// True when the first `tb` bytes of t and the first `ub` bytes of u share an address
+// (a NULL tensor shares none).
+bool overlaps(const sdu_tensor* t, size_t tb, const sdu_tensor* u, size_t ub) {
+    if (!t || !u) return false;
+    const uintptr_t p = (uintptr_t)t->t.ptr, q = (uintptr_t)u->t.ptr;
+    return p < q + ub && q < p + tb;
+}
+
+// A GEMM-shaped op's output against its inputs.  Tiles read rows and columns of A and
+// W that other tiles write when y overlaps them, so that is an argument error.  The
+// residual may be y itself, with the same row stride: each element is read and then
+// written by one thread.  A residual that only partly overlaps y is an error.
+bool gemm_output_aliases(const sdu_tensor* y, size_t yb, const sdu_tensor* a, size_t ab, const sdu_tensor* a2,
+                         size_t a2b, const sdu_tensor* w, size_t wb, const sdu_tensor* bias, size_t bb,
+                         const sdu_tensor* res, size_t rb) {
+    return overlaps(y, yb, a, ab) || overlaps(y, yb, a2, a2b) || overlaps(y, yb, w, wb) ||
+           overlaps(y, yb, bias, bb) || (res && dptr(res) != dptr(y) && overlaps(y, yb, res, rb));
+}
 
 int finish(sdu_ctx* ctx, hipError_t e, const char* what) {
     if (e != hipSuccess) return hipfail(ctx, e, what);
@@ -684,6 +704,10 @@ int sdu_matmul(sdu_ctx* ctx, const sdu_tensor* a, const sdu_tensor* a2, const sd
         (bias && !fits(bias, (size_t)N * 2)) || (residual && !fits(residual, (size_t)M * Nout * 2)) ||
         !fits(y, (size_t)M * Nout * (f32 ? 4 : 2)))
         return fail(ctx, SDU_ERR_ARG, "matmul tensor too small");
+    if (gemm_output_aliases(y, (size_t)M * Nout * (f32 ? 4 : 2), a, (size_t)M * K1 * 2, K2 ? a2 : nullptr,
+                            (size_t)M * K2 * 2, w, (size_t)N * K * 2, bias, (size_t)N * 2, residual,
+                            (size_t)M * Nout * 2))
+        return fail(ctx, SDU_ERR_ARG, "matmul output overlaps an input");
     GemmArgs g{};
     g.M = M; g.N = N; g.K = K;
     g.amode = A_DENSE;
@@ -716,6 +740,10 @@ int sdu_conv2d(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* w, const sdu
         (residual && !fits(residual, Mo * Co * 2)) || !fits(y, Mo * Co * (f32 ? 4 : 2)) ||
         (temb && temb->t.dtype != SDU_F32))
         return fail(ctx, SDU_ERR_ARG, "conv2d tensor too small");
+    if (gemm_output_aliases(y, Mo * Co * (f32 ? 4 : 2), x, (size_t)B * H * W * Ci * 2, nullptr, 0, w,
+                            (size_t)Co * ksize * ksize * Ci * 2, bias, (size_t)Co * 2, residual, Mo * Co * 2) ||
+        overlaps(y, Mo * Co * (f32 ? 4 : 2), temb, (size_t)Co * 4))
+        return fail(ctx, SDU_ERR_ARG, "conv2d output overlaps an input");
     GemmArgs g{};
     g.M = (int)Mo; g.N = Co;
     if (ksize == 1) {
@@ -754,6 +782,16 @@ int sdu_conv2d_groupnorm(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* w,
         !fits(y, M * Co * 2) || !fits(gamma, (size_t)Co * 2) || !fits(beta, (size_t)Co * 2) ||
         !fits(gn_y, M * Co * 2) || (temb && temb->t.dtype != SDU_F32))
         return fail(ctx, SDU_ERR_ARG, "conv2d_groupnorm tensor too small");
+    // gn_y may be y itself (the GroupNorm is elementwise once its statistics are formed;
+    // each element is read and then written by one thread) or any of the conv's inputs (it
+    // runs after the conv), but not gamma, beta or a shifted view of y
+    if (gemm_output_aliases(y, M * Co * 2, x, M * Ci * 2, nullptr, 0, w, (size_t)Co * 9 * Ci * 2, bias,
+                            (size_t)Co * 2, residual, M * Co * 2) ||
+        overlaps(y, M * Co * 2, temb, (size_t)Co * 4) || overlaps(y, M * Co * 2, gamma, (size_t)Co * 2) ||
+        overlaps(y, M * Co * 2, beta, (size_t)Co * 2) || overlaps(gn_y, M * Co * 2, gamma, (size_t)Co * 2) ||
+        overlaps(gn_y, M * Co * 2, beta, (size_t)Co * 2) ||
+        (dptr(gn_y) != dptr(y) && overlaps(gn_y, M * Co * 2, y, M * Co * 2)))
+        return fail(ctx, SDU_ERR_ARG, "conv2d_groupnorm output overlaps an input");
     GemmArgs g{};
     g.M = (int)M; g.N = Co; g.K = 9 * Ci;
     g.amode = A_CONV3;

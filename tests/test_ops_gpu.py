@@ -291,6 +291,56 @@ def test_conv2d(op_engine, B, H, W, Ci, Co, k, stride, ups, temb, res):
     assert np.abs(got - ref).max() < 3e-2
 
 
+@pytest.mark.parametrize("M,N,K", [
+    (8192, 320, 320),    # the attention output projection's shape (residual loaded up front)
+    (128, 1280, 5120),   # split K
+])
+def test_matmul_inplace_residual(op_engine, M, N, K):
+    """residual = y: the transformer's in-place residual adds (t += attn . Wo^T + b)."""
+    say(f"matmul in-place residual M={M} N={N} K={K}")
+    e = op_engine
+    a, w, bb, rr = r16((M, K), 51), r16((N, K), 52, 0.05), r16((N,), 53, 0.5), r16((M, N), 54)
+    ty = e.upload(rr.astype(np.float16))
+    e.matmul(e.upload(a.astype(np.float16)), e.upload(w.astype(np.float16)), ty, M, N, K,
+             bias=e.upload(bb.astype(np.float16)), residual=ty)
+    ref = (U.linear(t(a), t(w), t(bb)) + t(rr)).numpy()
+    got = ty.numpy().astype(np.float32)
+    assert rel_err_l1(got, ref) < 1e-3
+    assert np.abs(got - ref).max() < 3e-2
+
+
+def test_conv2d_inplace_residual_and_overlap_errors(op_engine):
+    """A conv's residual may be its output; an output over the conv's or a matmul's own
+    operands is an argument error (other tiles still read what it would overwrite)."""
+    import sdu
+    say("conv2d in-place residual; overlap errors")
+    e = op_engine
+    B, H, W, C = 2, 32, 32, 64
+    x, w, rr = r16((B, H, W, C), 61), r16((C, C, 3, 3), 62, 1.0 / math.sqrt(9 * C)), r16((B, H, W, C), 63)
+    tx = e.upload(x.astype(np.float16))
+    tw = e.upload(w.transpose(0, 2, 3, 1).astype(np.float16))
+    ty = e.upload(rr.astype(np.float16))
+    e.conv2d(tx, tw, ty, B, H, W, C, C, residual=ty)
+    ref = U.conv2d(t(x.transpose(0, 3, 1, 2)), t(w), None, stride=1, pad=1).numpy().transpose(0, 2, 3, 1) + rr
+    got = ty.numpy().astype(np.float32)
+    assert rel_err_l1(got, ref) < 1e-3
+    with pytest.raises(sdu.SduError) as ex:
+        e.conv2d(tx, tw, tx, B, H, W, C, C)  # y = x
+    assert ex.value.code == sdu.SDU_ERR_ARG
+    g, bt = e.upload(np.ones(C, np.float16)), e.upload(np.zeros(C, np.float16))
+    with pytest.raises(sdu.SduError) as ex:
+        e.conv2d_groupnorm(tx, tw, tx, g, bt, ty, B, H, W, C, C)  # conv output y = x
+    assert ex.value.code == sdu.SDU_ERR_ARG
+    ta = e.upload(r16((64, 64), 64).astype(np.float16))
+    tw2 = e.upload(r16((64, 64), 65, 0.1).astype(np.float16))
+    for y in (ta, tw2):
+        with pytest.raises(sdu.SduError) as ex:
+            e.matmul(ta, tw2, y, 64, 64, 64)  # y = a, y = w
+        assert ex.value.code == sdu.SDU_ERR_ARG
+    # the failed calls launched nothing: x still holds its input
+    assert np.array_equal(tx.numpy(), x.astype(np.float16))
+
+
 # ------------------------------------------------------------------ attention
 
 
