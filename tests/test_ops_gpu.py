@@ -361,6 +361,11 @@ def test_conv2d_inplace_residual_and_overlap_errors(op_engine):
     (1, 1, 33, 65, 56),
     (1, 2, 40, 50, 96),
     (1, 1, 20, 30, 120),
+    # the shared-tile kernel with ragged query and key counts (a last query block with
+    # 2 valid queries; last key tiles with 6, 13 and 60 valid keys)
+    (2, 8, 2050, 1030, 40),   # 128-key tiles (at most 512 blocks)
+    (4, 8, 4000, 333, 40),    # 64-key tiles
+    (4, 8, 1000, 700, 80),    # eight query waves per block
 ])
 def test_attention(op_engine, B, heads, Sq, Sk, d):
     say(f"attention B={B} heads={heads} Sq={Sq} Sk={Sk} d={d}")
