@@ -258,6 +258,10 @@ def test_matmul_split_repeat(op_engine):
     (1, 90, 90, 320, 320, 3, 1, False, True, True),
     (2, 62, 66, 320, 320, 3, 1, False, False, False),
     (1, 90, 90, 320, 312, 3, 1, False, True, True),    # last N tile partly outside N
+    # odd and ragged images on the other paths
+    (1, 5, 7, 64, 64, 3, 1, True, False, True),        # upsample 5x7 -> 10x14 (+ residual)
+    (1, 33, 31, 320, 640, 3, 2, False, True, False),   # stride 2 over odd sizes -> 17x16
+    (2, 17, 19, 640, 640, 3, 1, False, False, True),   # M = 646 at 640 channels
 ])
 def test_conv2d(op_engine, B, H, W, Ci, Co, k, stride, ups, temb, res):
     say(f"conv2d B={B} {H}x{W} {Ci}->{Co} k={k} s={stride} ups={ups} temb={temb} res={res}")
