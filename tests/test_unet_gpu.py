@@ -133,6 +133,19 @@ def test_forward_b3_40(unet_engine, oracle_weights):
     assert e <= TOL
 
 
+def test_forward_b2_72x56(unet_engine, oracle_weights):
+    """Non-square latent whose levels are 72x56, 36x28, 18x14 and 9x7: the first level
+    (4032 pixels, 31.5 row tiles per image) takes its GroupNorm statistics from the GEMM
+    epilogues, the bottom level has an odd 63 pixels, and the up path's 2x upsamples must
+    land back on 18x14 and 36x28."""
+    lat, temb, ctx = inputs(2, 72, 56, seed=19)
+    say("forward B=2 72x56")
+    got = unet_engine.forward(lat, temb, ctx)
+    e = rel_err_l1(got, oracle_forward(oracle_weights, lat, temb, ctx))
+    say(f"relErr B=2 72x56 = {e:.3e}")
+    assert e <= TOL
+
+
 @pytest.mark.slow
 def test_forward_b2_96(unet_engine, oracle_weights):
     """96x96 latent: 9216-token self-attention at hd 40."""
