@@ -38,6 +38,41 @@ hipError_t nchw_to_nhwc_launch(const float* src, f16* dst, int B, int Bsrc, int 
     return hipGetLastError();
 }
 
+// The UNet forward's inputs in one launch, outside its graph: the latent NCHW fp32
+// [B,C,H,W] -> NHWC fp16 [B,H,W,Cpad] (channels >= C zero), the context fp32 -> fp16,
+// and ntemb floats of the time projection copied.  Threads [0, nlat) take the latent,
+// the next nctx the context, the next ntemb the time projection.
+__global__ void stage_in_kernel(const float* lat, const float* ctx, const float* temb, f16* lat16, f16* ctx16,
+                                float* temb_dst, int B, int C, int Cpad, int HW, int64_t nctx, int ntemb) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t nlat = (int64_t)B * HW * Cpad;
+    if (i < nlat) {
+        const int c = (int)(i % Cpad);
+        const int64_t pix = i / Cpad;
+        const int b = (int)(pix / HW), p = (int)(pix % HW);
+        lat16[i] = (f16)(c < C ? lat[((int64_t)b * C + c) * HW + p] : 0.f);
+        return;
+    }
+    i -= nlat;
+    if (i < nctx) {
+        ctx16[i] = (f16)ctx[i];
+        return;
+    }
+    i -= nctx;
+    if (i < ntemb) temb_dst[i] = temb[i];
+}
+
+hipError_t stage_in_launch(const float* lat, const float* ctx, const float* temb, f16* lat16, f16* ctx16,
+                           float* temb_dst, int B, int C, int Cpad, int HW, int64_t nctx, int ntemb,
+                           hipStream_t s) {
+    const int64_t nlat = (int64_t)B * HW * Cpad, total = nlat + nctx + ntemb;
+    launch_timed("stage_in_kernel", 0.0, 4.0 * B * C * HW + 2.0 * nlat + 6.0 * nctx + 8.0 * ntemb, [&] {
+        SDU_LAUNCH(stage_in_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, lat, ctx, temb, lat16,
+                   ctx16, temb_dst, B, C, Cpad, HW, nctx, ntemb);
+    });
+    return hipGetLastError();
+}
+
 // One thread per 8 channels of one token.
 __global__ void embed_kernel(const int32_t* ids, const f16* tok, const f16* pos, f16* out, int B, int S, int C,
                              int vocab) {

@@ -187,6 +187,12 @@ hipError_t layernorm_launch(const f16* x, const f16* gamma, const f16* beta, f16
 // TAESD decoder's input clamp).
 hipError_t nchw_to_nhwc_launch(const float* src, f16* dst, int B, int Bsrc, int C, int Cpad, int HW,
                                hipStream_t s, int tanh_clamp = 0);
+// The UNet forward's inputs in one launch: latent NCHW fp32 [B,C,H,W] -> NHWC fp16
+// [B,H,W,Cpad], context fp32 -> fp16 (nctx values), ntemb time-projection floats copied
+// to temb_dst (ntemb 0: none).
+hipError_t stage_in_launch(const float* lat, const float* ctx, const float* temb, f16* lat16, f16* ctx16,
+                           float* temb_dst, int B, int C, int Cpad, int HW, int64_t nctx, int ntemb,
+                           hipStream_t s);
 // Token + position embedding: out[b*S + i][:] = tok[ids[b*S + i]][:] + pos[i][:] (fp16,
 // summed in fp32), ids clamped to [0, vocab).  C % 8 == 0.
 hipError_t embed_launch(const int32_t* ids, const f16* tok, const f16* pos, f16* out, int B, int S, int C,

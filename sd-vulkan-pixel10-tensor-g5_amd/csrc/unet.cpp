@@ -403,6 +403,10 @@ struct FwdState {
     float* in_ctx = nullptr;   // [B, L, 768]
     float* in_noise = nullptr; // denoise: [steps-1, 4, H, W]
     float* out = nullptr;      // forward: [B,4,H,W]; denoise: [4,H,W]
+    // forward: the graph's fp16 inputs (arena), filled before each replay by one
+    // stage_in launch from the caller's buffers
+    f16* lat16 = nullptr;      // [B,H,W,8]
+    f16* ctx16 = nullptr;      // [B,L,768]
     hipGraphExec_t exec = nullptr;
 };
 
@@ -410,12 +414,12 @@ static void body(Exec& E, FwdState& S) {
     const Fwd& F = S.f;
     const int HW = F.H * F.W;
     if (S.kind == 0) {
-        f16* lat = E.alloc<f16>((size_t)F.B * HW * kLatCpad);
-        f16* ctx16 = E.alloc<f16>((size_t)F.B * F.L * kCtxDim);
-        E.run("io", [&] { return nchw_to_nhwc_launch(S.in_lat, lat, F.B, F.B, kLatC, kLatCpad, HW, E.s); });
-        E.run("io", [&] { return f32_to_f16_launch(S.in_ctx, ctx16, (int64_t)F.B * F.L * kCtxDim, E.s); });
-        const f16* kv = cross_kv(E, ctx16, F.L);
-        unet_core(E, F, lat, S.in_temb, kv, S.out);
+        // the first two allocations, so every run of the body (sizing, capture, profile)
+        // places them at the same arena offsets
+        S.lat16 = E.alloc<f16>((size_t)F.B * HW * kLatCpad);
+        S.ctx16 = E.alloc<f16>((size_t)F.B * F.L * kCtxDim);
+        const f16* kv = cross_kv(E, S.ctx16, F.L);
+        unet_core(E, F, S.lat16, S.in_temb, kv, S.out);
         return;
     }
     // denoise: x (fp32 [4,H,W]) lives in `out`; B = 2 (cond, uncond)
@@ -565,6 +569,14 @@ static int check_shape(Ctx& c, int B, int H, int W, int L) {
     return SDU_OK;
 }
 
+// A forward state's inputs into its graph's fp16 buffers, in one launch (temb NULL: the
+// time projection is already in S.in_temb).
+static hipError_t stage_inputs(Ctx& c, const FwdState& S, const float* lat, const float* temb, const float* ctx) {
+    const Fwd& F = S.f;
+    return stage_in_launch(lat, ctx, temb, S.lat16, S.ctx16, S.in_temb, F.B, kLatC, kLatCpad, F.H * F.W,
+                           (int64_t)F.B * F.L * kCtxDim, temb ? 320 : 0, c.stream);
+}
+
 int unet_forward_device(Ctx& c, const float* d_lat, const float* d_temb, const float* d_ctx, int B, int H,
                         int W, int L, float* d_out) {
     int st = check_shape(c, B, H, W, L);
@@ -573,10 +585,7 @@ int unet_forward_device(Ctx& c, const float* d_lat, const float* d_temb, const f
     if (!S) return st;
     const size_t lat_b = (size_t)B * kLatC * H * W * 4;
     hipError_t e;
-    if ((e = hipMemcpyAsync(S->in_lat, d_lat, lat_b, hipMemcpyDeviceToDevice, c.stream)) ||
-        (e = hipMemcpyAsync(S->in_temb, d_temb, 320 * 4, hipMemcpyDeviceToDevice, c.stream)) ||
-        (e = hipMemcpyAsync(S->in_ctx, d_ctx, (size_t)B * L * kCtxDim * 4, hipMemcpyDeviceToDevice, c.stream)) ||
-        (e = hipGraphLaunch(S->exec, c.stream)) ||
+    if ((e = stage_inputs(c, *S, d_lat, d_temb, d_ctx)) || (e = hipGraphLaunch(S->exec, c.stream)) ||
         (e = hipMemcpyAsync(d_out, S->out, lat_b, hipMemcpyDeviceToDevice, c.stream)))
         return hip_fail(c, e, "forward");
     return SDU_OK;
@@ -593,7 +602,7 @@ int unet_forward_host(Ctx& c, const float* lat, const float* temb, const float* 
     if ((e = hipMemcpyAsync(S->in_lat, lat, lat_b, hipMemcpyHostToDevice, c.stream)) ||
         (e = hipMemcpyAsync(S->in_temb, temb, 320 * 4, hipMemcpyHostToDevice, c.stream)) ||
         (e = hipMemcpyAsync(S->in_ctx, ctx, (size_t)B * L * kCtxDim * 4, hipMemcpyHostToDevice, c.stream)) ||
-        (e = hipGraphLaunch(S->exec, c.stream)) ||
+        (e = stage_inputs(c, *S, S->in_lat, nullptr, S->in_ctx)) || (e = hipGraphLaunch(S->exec, c.stream)) ||
         (e = hipMemcpyAsync(out, S->out, lat_b, hipMemcpyDeviceToHost, c.stream)) ||
         (e = hipStreamSynchronize(c.stream)))
         return hip_fail(c, e, "forward");
