@@ -21,6 +21,8 @@
 // and runs the epilogue (few splits), or a reduce kernel does (many splits).
 #include "sdu_internal.h"
 
+#include <cstdio>
+
 #include <algorithm>
 
 namespace sdu {
@@ -1274,19 +1276,26 @@ __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)
 // ..., with all of a chunk's row loads issued together.  K % 8 == 0, K <= GV_MAXK.
 static constexpr int GV_ROWS = 4;
 static constexpr int GV_MAXK = 2048;
+// NV vectors at once (x [NV][K], y [NV][N]): each weight row is read once for all of
+// them; every vector's sums run in the same order as with NV = 1.
+template <int NV>
 __global__ __launch_bounds__(256) void gemv_kernel(const float* x, const f16* W, const f16* bias,
                                                    float* y, int N, int K, int act_in, int act_out) {
-    __shared__ __attribute__((aligned(16))) float xs[GV_MAXK];
-    for (int k = threadIdx.x; k < K; k += 256) {
-        const float v = x[k];
-        xs[k] = act_in ? silu_f(v) : v;
-    }
+    __shared__ __attribute__((aligned(16))) float xs[NV][GV_MAXK];
+    for (int k = threadIdx.x; k < K; k += 256)
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            const float t = x[(int64_t)v * K + k];
+            xs[v][k] = act_in ? silu_f(t) : t;
+        }
     __syncthreads();
     const int lane = threadIdx.x & 63;
     const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * GV_ROWS;
-    float s[GV_ROWS];
+    float s[GV_ROWS][NV];
 #pragma unroll
-    for (int r = 0; r < GV_ROWS; ++r) s[r] = 0.f;
+    for (int r = 0; r < GV_ROWS; ++r)
+#pragma unroll
+        for (int v = 0; v < NV; ++v) s[r][v] = 0.f;
 #pragma unroll
     for (int j = 0; j < GV_MAXK / 512; ++j) {
         const int k = (lane + 64 * j) * 8;
@@ -1294,36 +1303,51 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* x, const f16* W,
         uint4 wv[GV_ROWS];
 #pragma unroll
         for (int r = 0; r < GV_ROWS; ++r) wv[r] = *(const uint4*)(W + (int64_t)min(row0 + r, N - 1) * K + k);
-        const float4 x0 = *(const float4*)&xs[k], x1 = *(const float4*)&xs[k + 4];
-        const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
-        for (int r = 0; r < GV_ROWS; ++r) {
-            const f16* wh = (const f16*)&wv[r];
+        for (int v = 0; v < NV; ++v) {
+            const float4 x0 = *(const float4*)&xs[v][k], x1 = *(const float4*)&xs[v][k + 4];
+            const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
-            for (int i = 0; i < 8; ++i) s[r] += xv[i] * (float)wh[i];
+            for (int r = 0; r < GV_ROWS; ++r) {
+                const f16* wh = (const f16*)&wv[r];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) s[r][v] += xv[i] * (float)wh[i];
+            }
         }
     }
 #pragma unroll
-    for (int r = 0; r < GV_ROWS; ++r) {
-        float t = s[r];
+    for (int r = 0; r < GV_ROWS; ++r)
 #pragma unroll
-        for (int off = 32; off > 0; off >>= 1) t += __shfl_xor(t, off);
-        const int n = row0 + r;
-        if (lane == 0 && n < N) {
-            if (bias) t += (float)bias[n];
-            if (act_out) t = silu_f(t);
-            y[n] = t;
+        for (int v = 0; v < NV; ++v) {
+            float t = s[r][v];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) t += __shfl_xor(t, off);
+            const int n = row0 + r;
+            if (lane == 0 && n < N) {
+                if (bias) t += (float)bias[n];
+                if (act_out) t = silu_f(t);
+                y[(int64_t)v * N + n] = t;
+            }
         }
-    }
 }
 
 hipError_t gemv_launch(const float* x, const f16* W, const f16* bias, float* y, int N, int K,
-                       int act_in, int act_out, hipStream_t s) {
-    if (N <= 0 || K <= 0 || K % 8 || K > GV_MAXK) return hipErrorInvalidValue;
-    launch_timed("gemv_kernel", 2.0 * N * K, 2.0 * N * K + 4.0 * (N + K), [&] {
-        SDU_LAUNCH(gemv_kernel, dim3((N + 4 * GV_ROWS - 1) / (4 * GV_ROWS)), dim3(256), 0, s, x, W, bias, y,
-                           N, K, act_in, act_out);
-    });
+                       int act_in, int act_out, hipStream_t s, int nvec) {
+    if (N <= 0 || K <= 0 || K % 8 || K > GV_MAXK || nvec < 1) return hipErrorInvalidValue;
+    const dim3 grid((N + 4 * GV_ROWS - 1) / (4 * GV_ROWS));
+    for (int v0 = 0; v0 < nvec;) {
+        const int nv = nvec - v0 >= 4 ? 4 : nvec - v0 >= 2 ? 2 : 1;
+        const float* xv = x + (int64_t)v0 * K;
+        float* yv = y + (int64_t)v0 * N;
+        char name[24];
+        snprintf(name, sizeof name, "gemv_kernel<%d>", nv);
+        launch_timed(name, 2.0 * nv * N * K, 2.0 * N * K + 4.0 * nv * (N + K), [&] {
+            if (nv == 4) SDU_LAUNCH(gemv_kernel<4>, grid, dim3(256), 0, s, xv, W, bias, yv, N, K, act_in, act_out);
+            else if (nv == 2) SDU_LAUNCH(gemv_kernel<2>, grid, dim3(256), 0, s, xv, W, bias, yv, N, K, act_in, act_out);
+            else SDU_LAUNCH(gemv_kernel<1>, grid, dim3(256), 0, s, xv, W, bias, yv, N, K, act_in, act_out);
+        });
+        v0 += nv;
+    }
     return hipGetLastError();
 }
 

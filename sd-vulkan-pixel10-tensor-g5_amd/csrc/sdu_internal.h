@@ -150,9 +150,10 @@ hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s);
 hipError_t splitk_reduce_launch(const GemmArgs& a, double bytes, hipStream_t s);
 
 // y[n] = act_out( sum_k act_in(x[k]) * W[n,k] + bias[n] ), fp32 in/out, W fp16 [N,K].
-// act: 0 none, 1 SiLU.
+// act: 0 none, 1 SiLU.  nvec vectors: x [nvec][K] -> y [nvec][N], up to 4 per launch
+// sharing each weight read; every vector's result equals its own nvec = 1 call.
 hipError_t gemv_launch(const float* x, const f16* W, const f16* bias, float* y, int N, int K,
-                       int act_in, int act_out, hipStream_t s);
+                       int act_in, int act_out, hipStream_t s, int nvec = 1);
 
 // ----------------------------------------------------------------- attention
 struct AttnArgs {

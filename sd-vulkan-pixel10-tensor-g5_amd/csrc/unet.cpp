@@ -219,21 +219,23 @@ static Act conv3_block(Exec& E, const std::string& pf, const f16* x, int H, int 
 
 // time MLP (vk_engine.cpp:716-717) + every resnet's time_emb_proj(silu(temb)) in
 // one GEMV over the fused projection block.  Returns tproj [tproj_total] fp32.
-static float* time_embed(Exec& E, const float* temb320) {
+// n time embeddings at once (temb320 [n][320] -> [n][tproj_total]): the steps of a
+// denoise share each weight read.
+static float* time_embed(Exec& E, const float* temb320, int n = 1) {
     Ctx& c = E.c;
-    float* t1 = E.alloc<float>(1280);
-    float* temb = E.alloc<float>(1280);
-    float* tproj = E.alloc<float>(c.tproj_total);
+    float* t1 = E.alloc<float>((size_t)n * 1280);
+    float* temb = E.alloc<float>((size_t)n * 1280);
+    float* tproj = E.alloc<float>((size_t)n * c.tproj_total);
     E.run("time_mlp", [&] {
         return gemv_launch(temb320, c.wd("time_embedding.linear_1.weight"), c.wd("time_embedding.linear_1.bias"),
-                           t1, 1280, 320, 0, 1, E.s);
+                           t1, 1280, 320, 0, 1, E.s, n);
     });
     E.run("time_mlp", [&] {
         return gemv_launch(t1, c.wd("time_embedding.linear_2.weight"), c.wd("time_embedding.linear_2.bias"),
-                           temb, 1280, 1280, 0, 0, E.s);
+                           temb, 1280, 1280, 0, 0, E.s, n);
     });
     E.run("time_mlp", [&] {
-        return gemv_launch(temb, c.w_tproj, c.b_tproj, tproj, c.tproj_total, 1280, 1, 0, E.s);
+        return gemv_launch(temb, c.w_tproj, c.b_tproj, tproj, c.tproj_total, 1280, 1, 0, E.s, n);
     });
     return tproj;
 }
@@ -248,8 +250,10 @@ static f16* cross_kv(Exec& E, const f16* ctx16, int L) {
 }
 
 // UNet body: lat NHWC fp16 [B,H,W,8] -> eps fp32 NCHW [B,4,H,W] (vk_engine.cpp:711-790).
+// tproj_pre: the time projections of this forward when already computed (a denoise
+// computes every step's at once); otherwise they are formed here from temb320.
 static void unet_core(Exec& E, const Fwd& F, const f16* lat, const float* temb320, const f16* kv,
-                      float* out) {
+                      float* out, const float* tproj_pre = nullptr) {
     Ctx& c = E.c;
     const size_t mk0 = E.ar->mark();
     // GroupNorm accumulators of this forward (2 per resnet, 1 per transformer, conv_norm_out)
@@ -270,7 +274,7 @@ static void unet_core(Exec& E, const Fwd& F, const f16* lat, const float* temb32
         void* p = E.gn_acc;
         E.run("groupnorm", [&] { return zero_launch(p, (acc_n + st_n) * sizeof(double), E.s); });
     }
-    const float* tproj = time_embed(E, temb320);
+    const float* tproj = tproj_pre ? tproj_pre : time_embed(E, temb320);
     int H = F.H, Wd = F.W;
     struct Skip { Act a; int ch; };
     std::vector<Skip> skips;
@@ -434,6 +438,8 @@ static void body(Exec& E, FwdState& S) {
     });
     E.run("io", [&] { return f32_to_f16_launch(S.in_ctx, ctx16, (int64_t)2 * F.L * kCtxDim, E.s); });
     const f16* kv = cross_kv(E, ctx16, F.L);  // context is fixed across steps
+    // every step's time MLP and resnet time projections in one pass
+    const float* tproj_all = time_embed(E, S.in_temb, S.steps);
     LcmSched sched(S.steps);
     for (int i = 0; i < S.steps; ++i) {
         // TpuUnetPipeline.kt:94-99: CFG on the first cfg_steps steps, then one forward on
@@ -442,7 +448,7 @@ static void body(Exec& E, FwdState& S) {
         E.B = cfg ? 2 : 1;
         Fwd Fi = F;
         Fi.B = E.B;
-        unet_core(E, Fi, lat, S.in_temb + (size_t)i * 320, kv, eps2);
+        unet_core(E, Fi, lat, nullptr, kv, eps2, tproj_all + (size_t)i * E.c.tproj_total);
         E.B = 2;
         LcmCoeffs co = sched.coeffs(i, 0.f);
         co.guidance_dev = S.d_guidance;
