@@ -55,13 +55,16 @@ bool overlaps(const sdu_tensor* t, size_t tb, const sdu_tensor* u, size_t ub) {
 
 // A GEMM-shaped op's output against its inputs.  Tiles read rows and columns of A and
 // W that other tiles write when y overlaps them, so that is an argument error.  The
-// residual may be y itself, with the same row stride: each element is read and then
-// written by one thread.  A residual that only partly overlaps y is an error.
+// residual may be y itself when the output is fp16 (same element size and row stride):
+// each element is read and then written by one thread.  With an fp32 output, a store
+// of row m covers the fp16 residual of rows 2m and 2m + 1, which other tiles still
+// read, so any overlap is an error; so is a residual that only partly overlaps y.
 bool gemm_output_aliases(const sdu_tensor* y, size_t yb, const sdu_tensor* a, size_t ab, const sdu_tensor* a2,
                          size_t a2b, const sdu_tensor* w, size_t wb, const sdu_tensor* bias, size_t bb,
-                         const sdu_tensor* res, size_t rb) {
+                         const sdu_tensor* res, size_t rb, bool out_f32) {
+    const bool res_in_place = !out_f32 && res && dptr(res) == dptr(y);
     return overlaps(y, yb, a, ab) || overlaps(y, yb, a2, a2b) || overlaps(y, yb, w, wb) ||
-           overlaps(y, yb, bias, bb) || (res && dptr(res) != dptr(y) && overlaps(y, yb, res, rb));
+           overlaps(y, yb, bias, bb) || (res && !res_in_place && overlaps(y, yb, res, rb));
 }
 
 int finish(sdu_ctx* ctx, hipError_t e, const char* what) {
@@ -706,7 +709,7 @@ int sdu_matmul(sdu_ctx* ctx, const sdu_tensor* a, const sdu_tensor* a2, const sd
         return fail(ctx, SDU_ERR_ARG, "matmul tensor too small");
     if (gemm_output_aliases(y, (size_t)M * Nout * (f32 ? 4 : 2), a, (size_t)M * K1 * 2, K2 ? a2 : nullptr,
                             (size_t)M * K2 * 2, w, (size_t)N * K * 2, bias, (size_t)N * 2, residual,
-                            (size_t)M * Nout * 2))
+                            (size_t)M * Nout * 2, f32 != 0))
         return fail(ctx, SDU_ERR_ARG, "matmul output overlaps an input");
     GemmArgs g{};
     g.M = M; g.N = N; g.K = K;
@@ -741,7 +744,8 @@ int sdu_conv2d(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* w, const sdu
         (temb && temb->t.dtype != SDU_F32))
         return fail(ctx, SDU_ERR_ARG, "conv2d tensor too small");
     if (gemm_output_aliases(y, Mo * Co * (f32 ? 4 : 2), x, (size_t)B * H * W * Ci * 2, nullptr, 0, w,
-                            (size_t)Co * ksize * ksize * Ci * 2, bias, (size_t)Co * 2, residual, Mo * Co * 2) ||
+                            (size_t)Co * ksize * ksize * Ci * 2, bias, (size_t)Co * 2, residual, Mo * Co * 2,
+                            f32 != 0) ||
         overlaps(y, Mo * Co * (f32 ? 4 : 2), temb, (size_t)Co * 4))
         return fail(ctx, SDU_ERR_ARG, "conv2d output overlaps an input");
     GemmArgs g{};
@@ -786,7 +790,7 @@ int sdu_conv2d_groupnorm(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* w,
     // each element is read and then written by one thread) or any of the conv's inputs (it
     // runs after the conv), but not gamma, beta or a shifted view of y
     if (gemm_output_aliases(y, M * Co * 2, x, M * Ci * 2, nullptr, 0, w, (size_t)Co * 9 * Ci * 2, bias,
-                            (size_t)Co * 2, residual, M * Co * 2) ||
+                            (size_t)Co * 2, residual, M * Co * 2, false) ||
         overlaps(y, M * Co * 2, temb, (size_t)Co * 4) || overlaps(y, M * Co * 2, gamma, (size_t)Co * 2) ||
         overlaps(y, M * Co * 2, beta, (size_t)Co * 2) || overlaps(gn_y, M * Co * 2, gamma, (size_t)Co * 2) ||
         overlaps(gn_y, M * Co * 2, beta, (size_t)Co * 2) ||

@@ -15,9 +15,11 @@
 // skip concat, vk_engine.cpp:678-688), so the concat is never materialised.
 // When one (image, group) slab is small (HW * C/G <= 32K elements: the 32x32 and
 // smaller levels of the 64x64 UNet) and fits the registers of a 512-thread block,
-// a single kernel does it all: the slab is loaded once, mean and variance are
-// reduced exactly in two passes over the registers, and the normalised values are
-// stored -- one launch, one read and one write of the tensor.
+// a single kernel does it all: the slab is loaded once into registers, the sums and
+// sums of squares of x minus the group's first value are reduced in one pass (the
+// shift keeps the one-pass variance free of cancellation when the mean dwarfs the
+// spread), and the normalised values are stored -- one launch, one read and one
+// write of the tensor.
 //
 // LayerNorm replaces layernorm_f32.comp (vk_engine.cpp:652): one wave per token,
 // exact two-pass mean / variance in registers.

@@ -341,6 +341,20 @@ def test_conv2d_inplace_residual_and_overlap_errors(op_engine):
         with pytest.raises(sdu.SduError) as ex:
             e.matmul(ta, tw2, y, 64, 64, 64)  # y = a, y = w
         assert ex.value.code == sdu.SDU_ERR_ARG
+    # an fp32 output over its own fp16 residual: a row's fp32 store would cover the
+    # residual of two other rows, so even residual == y is an error with SDU_EPI_OUT_F32
+    ty32 = e.tensor((B, H, W, C), sdu.SDU_F32)
+    tr32 = e.upload(rr.astype(np.float16))
+    with pytest.raises(sdu.SduError) as ex:
+        e.conv2d(tx, tw, ty32, B, H, W, C, C, residual=ty32, flags=sdu.SDU_EPI_OUT_F32)
+    assert ex.value.code == sdu.SDU_ERR_ARG
+    tm32 = e.tensor((64, 64), sdu.SDU_F32)
+    with pytest.raises(sdu.SduError) as ex:
+        e.matmul(ta, tw2, tm32, 64, 64, 64, residual=tm32, flags=sdu.SDU_EPI_OUT_F32)
+    assert ex.value.code == sdu.SDU_ERR_ARG
+    # ... while an fp32 output with a separate fp16 residual is fine
+    e.conv2d(tx, tw, ty32, B, H, W, C, C, residual=tr32, flags=sdu.SDU_EPI_OUT_F32)
+    assert rel_err_l1(ty32.numpy(), ref) < 1e-3
     # the failed calls launched nothing: x still holds its input
     assert np.array_equal(tx.numpy(), x.astype(np.float16))
 
