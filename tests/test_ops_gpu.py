@@ -90,13 +90,23 @@ def test_groupnorm_large_mean(op_engine, B, H, W, C, silu):
     (2, 64, 64, 320, 320, 100.0, False, False, True),  # output mean 100x its spread
     (3, 40, 40, 64, 640, 30.0, False, True, False),    # 1600-pixel images: tiles straddle two
     (1, 8, 8, 128, 320, 50.0, True, False, True),      # 64-pixel images
+    # the UNet's smaller levels (split-K convs; the statistics from the in-kernel split sum)
+    (2, 8, 8, 1280, 1280, 0.0, True, False, True),     # 8x8 resnet conv1 -> norm2
+    (2, 16, 16, 1280, 1280, 30.0, False, True, False),  # 16x16 conv2 (+residual) -> GroupNorm
+    (2, 32, 32, 640, 640, 100.0, True, False, True),   # 32x32, output mean 100x its spread
+    (1, 32, 32, 640, 960, 0.0, False, True, True),     # 30 channels per group: 2 per thread
+    (2, 16, 16, 640, 1920, 0.0, True, False, True),    # 60 channels per group: 4 per thread
+    (1, 16, 16, 640, 2560, 10.0, False, False, True),  # 80 channels per group, 8 pixel rounds
+    (3, 8, 8, 1280, 1280, 5.0, True, True, True),      # odd batch
 ])
 def test_conv_groupnorm_epilogue_stats(op_engine, B, H, W, Ci, Co, mean, temb, res, silu):
     """The UNet's 64x64-level GroupNorm path: per-channel sums and sums of squares of the
     conv's stored fp16 output, kept by the GEMM epilogue (fp32 per tile, fp64 across tiles),
     then the GroupNorm from them.  The conv output is checked against the fp32 conv; the
     GroupNorm against an fp64 GroupNorm of the same fp16 conv output, so the check isolates
-    the statistics.  A large output mean is the case where E[x^2] - mean^2 cancels."""
+    the statistics.  A large output mean is the case where E[x^2] - mean^2 cancels.  The
+    smaller shapes split K, so their statistics come from the in-kernel split sum's
+    epilogue (60 and 80 channels per group, odd batch)."""
     say(f"conv+groupnorm B={B} {H}x{W} {Ci}->{Co} mean={mean} temb={temb} res={res} silu={silu}")
     e = op_engine
     HW = H * W
@@ -478,10 +488,12 @@ def test_op_argument_errors(op_engine):
         e.attention(a, a, a, a, 1, 1, 4, 4, 168, 168, 168, 168, 168, 1.0)  # d > 160
     with pytest.raises(sdu.SduError):
         e.groupnorm(a, a, a, a, 1, 16, 12, 0)  # C not a multiple of 8
-    big = e.tensor((1, 10, 10, 64))
-    with pytest.raises(sdu.SduError) as ex:  # 100-pixel images: a 128-row tile spans three
-        e.conv2d_groupnorm(big, e.tensor((64, 3, 3, 64)), big, e.tensor((64,)), e.tensor((64,)), big,
-                           1, 10, 10, 64, 64)
+    # 100-pixel images (a 128-row tile spans three) with 3 channels per group (odd: no
+    # single-kernel GroupNorm either)
+    xs, ys, gs = e.tensor((1, 10, 10, 96)), e.tensor((1, 10, 10, 96)), e.tensor((1, 10, 10, 96))
+    with pytest.raises(sdu.SduError) as ex:
+        e.conv2d_groupnorm(xs, e.tensor((96, 3, 3, 96)), ys, e.tensor((96,)), e.tensor((96,)), gs,
+                           1, 10, 10, 96, 96)
     assert ex.value.code == sdu.SDU_ERR_ARG
     with pytest.raises(sdu.SduError):
         e.forward(np.zeros((1, 4, 64, 64), np.float32), np.zeros(320, np.float32),
