@@ -142,6 +142,105 @@ def time_image_path(eng, sdu, rng, reps):
             "reps": reps, "weights": "seeded random (CLIP N(0,0.02), TAESD convs N(0,0.04))"}
 
 
+# The reference's own micro-benchmark shapes (VulkanBench.kt:72-118), timed per op with
+# each kernel's start / stop events (sdu_profile_ops), with the reference's Pixel 10 / Tensor
+# G5 figures beside them (README.md:235-244, docs/bench_screen.png; fp32 Vulkan).  matmul
+# shapes are M x N x K of C[M,N] = A[M,K] W^T; the split-K shapes are the 16x16 / 8x8 conv
+# GEMMs (reference M = Cout 1280, N = 256 / 64 pixels, K = 9 Cin) as pixels x Cout x K.
+# B = 1 throughout, 8 heads for attention, as the reference's bench.
+REF_OPS = [
+    ("mm_4096x2560x320", "matmul", dict(M=4096, N=2560, K=320), {"gflops": 248}),
+    ("mm_4096x320x1280", "matmul", dict(M=4096, N=320, K=1280), {"gflops": 219}),
+    ("mm_2048x2048x2048", "matmul", dict(M=2048, N=2048, K=2048), {"gflops": 245}),
+    ("splitk_1280x256x11520", "matmul", dict(M=256, N=1280, K=11520), {}),
+    ("splitk_1280x64x11520", "matmul", dict(M=64, N=1280, K=11520), {}),
+    ("conv_320to320_64x64", "conv", dict(H=64, C=320), {"gflops_im2col": 169, "gflops_winograd": 580}),
+    ("conv_640to640_32x32", "conv", dict(H=32, C=640), {"gflops_im2col": 197, "gflops_winograd": 392}),
+    ("conv_1280to1280_16x16", "conv", dict(H=16, C=1280), {"gflops_im2col": 186, "gflops_winograd": 114}),
+    ("silu_320x64x64", "silu", dict(n=320 * 64 * 64), {"ms": 1.72}),
+    ("groupnorm_320x64x64_g32", "groupnorm", dict(HW=64 * 64, C=320), {"ms": 2.14}),
+    ("groupnorm_1280x16x16_g32", "groupnorm", dict(HW=16 * 16, C=1280), {"ms": 1.04}),
+    ("attn_self_4096_d40", "attention", dict(Sq=4096, Sk=4096, d=40), {"ms": 187.0}),
+    ("attn_cross_4096x77_d40", "attention", dict(Sq=4096, Sk=77, d=40), {"ms": 10.6}),
+    ("attn_d80_s1024", "attention", dict(Sq=1024, Sk=1024, d=80), {"ms": 82.2}),
+    ("attn_d160_s256", "attention", dict(Sq=256, Sk=256, d=160), {"ms": 15.9}),
+]
+
+
+def roofline_frac(flops, nbytes, ms):
+    """max(FLOP / MFMA peak, bytes / HBM peak) over the measured time (the per-op roofline)."""
+    if ms <= 0:
+        return None
+    ideal_ms = max(flops / (PEAK_MFMA_TFLOPS * 1e12), nbytes / (PEAK_HBM_GBS * 1e9)) * 1e3
+    return round(ideal_ms / ms, 4)
+
+
+def time_reference_ops(sdu, reps=20):
+    """Each of REF_OPS timed on its own: 2 untimed calls, then `reps` calls inside an
+    sdu_profile_ops window.  The op's time is the sum of its kernels' event times per call,
+    without the fill kernel that clears the op-level scratch (zero_kernel: the UNet graph
+    clears its statistics once per forward, not per op)."""
+    import numpy as np
+    rng = np.random.default_rng(7)
+    eng = sdu.Engine(flags=sdu.SDU_INIT_NO_WEIGHTS)
+
+    def f16(shape, scale=1.0):
+        return eng.upload((rng.standard_normal(shape) * scale).astype(np.float16))
+
+    out = {}
+    try:
+        for name, kind, p, ref in REF_OPS:
+            if kind == "matmul":
+                M, N, K = p["M"], p["N"], p["K"]
+                a, w, y = f16((M, K)), f16((N, K), 1.0 / np.sqrt(K)), eng.tensor((M, N))
+                call = lambda: eng.matmul(a, w, y, M, N, K)
+                flops, nbytes = 2.0 * M * N * K, 2.0 * (M * K + N * K + M * N)
+            elif kind == "conv":
+                H, C = p["H"], p["C"]
+                x, w, y = f16((1, H, H, C)), f16((C, 3, 3, C), 1.0 / np.sqrt(9 * C)), eng.tensor((1, H, H, C))
+                call = lambda: eng.conv2d(x, w, y, 1, H, H, C, C)
+                flops, nbytes = 2.0 * H * H * C * C * 9, 2.0 * (2 * H * H * C + 9 * C * C)
+            elif kind == "silu":
+                n = p["n"]
+                x, y = f16((n,)), eng.tensor((n,))
+                call = lambda: eng.silu(x, y, n)
+                flops, nbytes = 0.0, 4.0 * n
+            elif kind == "groupnorm":
+                HW, C = p["HW"], p["C"]
+                x, g, b, y = f16((HW, C)), f16((C,)), f16((C,)), eng.tensor((HW, C))
+                call = lambda: eng.groupnorm(x, g, b, y, 1, HW, C)
+                flops, nbytes = 0.0, 4.0 * HW * C
+            else:
+                Sq, Sk, d = p["Sq"], p["Sk"], p["d"]
+                q, k, v, o = f16((Sq, 8 * d)), f16((Sk, 8 * d)), f16((Sk, 8 * d)), eng.tensor((Sq, 8 * d))
+                call = lambda: eng.attention(q, k, v, o, 1, 8, Sq, Sk, d, 8 * d, 8 * d, 8 * d, 8 * d,
+                                             1.0 / np.sqrt(d))
+                flops, nbytes = 4.0 * 8 * Sq * Sk * d, 2.0 * 8 * d * (2 * Sq + 2 * Sk)
+            for _ in range(2):
+                call()
+            eng.sync()
+            eng.profile_ops(True)
+            for _ in range(reps):
+                call()
+            prof, _ = eng.profile_ops(False)
+            kern = {k[2:]: v for k, v in prof.items() if k.startswith("k:") and k != "k:zero_kernel"}
+            ms = sum(v["ms"] for v in kern.values()) / reps
+            e = {"ms": round(ms, 5), "kernels": sorted(kern)}
+            if flops > 0:
+                e["tflops"] = round(flops / (ms * 1e-3) / 1e12, 1)
+                e["frac_mfma"] = round(e["tflops"] / PEAK_MFMA_TFLOPS, 4)
+            else:
+                e["gbs"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+                e["frac_hbm"] = round(e["gbs"] / PEAK_HBM_GBS, 4)
+            e["frac_roofline"] = roofline_frac(flops, nbytes, ms)
+            if ref:
+                e["pixel10_fp32"] = ref
+            out[name] = e
+    finally:
+        eng.release()
+    return out
+
+
 def measured_traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary
     (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by what the counter reads for
@@ -171,7 +270,14 @@ def main():
     ap.add_argument("--only", default="", metavar="B,H",
                     help="only time `steps` forwards at batch B and H x H latents (marked "
                          "timed_b<B>_<H>x<H>, for profiler runs), print one JSON line and exit")
+    ap.add_argument("--ref-ops", action="store_true",
+                    help="only time the reference's micro-benchmark shapes (REF_OPS), print one JSON "
+                         "line and exit")
     args = ap.parse_args()
+    if args.ref_ops:
+        import sdu
+        print(json.dumps({"reference_bench_ops": time_reference_ops(sdu)}), flush=True)
+        return
     if args.copy_probe:
         import torch
         n = args.copy_probe << 20
@@ -297,20 +403,25 @@ def main():
         roof["frac_of_measured_copy"] = round(roof["achieved"] / cal["copy_gbs"], 4)
     traffic = measured_traffic(dom_name)
     roof.update({"traffic": traffic, "kernel": dom_name, "calls": dom["calls"],
+                 "frac_roofline": roofline_frac(dom["flops"], dom["bytes"], dom["ms"]),
                  "timing": "start/stop HIP events of each launch (hipExtLaunchKernelGGL) on the engine "
                            "stream, one eager forward, each kernel once",
                  "flops_per_launch": dom["flops"] / dom["calls"],
                  "bytes_per_launch": dom["bytes"] / dom["calls"],
                  "avg_launch_us": round(avg_us, 3)})
+    # per kernel: the MFMA or HBM rate of its algorithmic FLOPs / bytes (split-K partials are
+    # overhead, counted nowhere: the reduce launch reports none), and frac_roofline = per-op
+    # roofline time max(FLOP / 2.5 PF, bytes / 8 TB/s) over the measured time, summed per launch
     per_kernel = {}
     for k, v in sorted(kernels.items(), key=lambda kv: -kv[1]["ms"]):
         e = {"calls": v["calls"], "ms": round(v["ms"], 4)}
         if v["flops"] > 0:
             e["tflops"] = round(v["flops"] / (v["ms"] * 1e-3) / 1e12, 1)
             e["frac_mfma"] = round(e["tflops"] / PEAK_MFMA_TFLOPS, 4)
-        elif v["bytes"] > 0:
+        if v["bytes"] > 0:
             e["gbs"] = round(v["bytes"] / (v["ms"] * 1e-3) / 1e9, 1)
             e["frac_hbm"] = round(e["gbs"] / PEAK_HBM_GBS, 4)
+        e["frac_roofline"] = roofline_frac(v["flops"], v["bytes"], v["ms"])
         per_kernel[k] = e
     # per op category (all kernels of the op, e.g. every conv 3x3 GEMM tile shape and its
     # split-K reduce): algorithmic FLOPs or bytes over the category's summed launch times
@@ -321,6 +432,7 @@ def main():
             e["frac_mfma"] = round(v["flops"] / (v["ms"] * 1e-3) / 1e12 / PEAK_MFMA_TFLOPS, 4)
         elif v["bytes"] > 0:
             e["frac_hbm"] = round(v["bytes"] / (v["ms"] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)
+        e["frac_roofline"] = roofline_frac(v["flops"], v["bytes"], v["ms"])
         per_cat[k] = e
 
     # the other single-GPU shapes: B=2 96x96 (9216-token attention) and B=16 64x64
@@ -333,8 +445,9 @@ def main():
                                     "roofline_ideal_ms": ideal, "frac_of_roofline": round(ideal / ms, 4)}
 
     image_path = time_image_path(eng, sdu, rng, max(5, args.steps // 5))
-    cpu = None if args.no_cpu else cpu_baseline()
     eng.release()
+    ref_ops = time_reference_ops(sdu)
+    cpu = None if args.no_cpu else cpu_baseline()
 
     line = {
         "metric": METRIC,
@@ -364,6 +477,7 @@ def main():
         "kernels": per_kernel,
         "categories": per_cat,
         "image_path": image_path,
+        "reference_bench_ops": ref_ops,
     }
     print(json.dumps(line), flush=True)
 

@@ -201,6 +201,18 @@ typedef struct sdu_prof_entry {
 } sdu_prof_entry;
 int sdu_profile(sdu_ctx* ctx, int B, int H, int W, int L, sdu_prof_entry* out,
                 int max_entries, int* n_entries, double* total_ms);
+/* Kernel timing of op-level calls, the counterpart of the reference's per-shader
+ * micro-benchmarks (VulkanBench.kt:66-126 over vk_engine.cpp:226-420, :1017-1218, which
+ * time one shader at fixed shapes).  enable = 1 opens a window: every kernel that the
+ * op-level entry points (sdu_matmul, sdu_conv2d, sdu_conv2d_groupnorm, sdu_groupnorm,
+ * sdu_groupnorm_noalloc, sdu_layernorm, sdu_attention(_ex), sdu_geglu, sdu_silu, sdu_add,
+ * sdu_add_bias, sdu_lcm_step) launch from then on carries its own start / stop events, as
+ * in sdu_profile.  enable = 0 closes the window: synchronises the stream and returns the
+ * entries accumulated per op ("matmul", ...) and per kernel ("k:" + kernel name), with
+ * total_ms summing the ops.  UNet / TAESD / CLIP calls made meanwhile are not timed.
+ * Closing a window that was not opened is SDU_ERR_ARG. */
+int sdu_profile_ops(sdu_ctx* ctx, int enable, sdu_prof_entry* out, int max_entries, int* n_entries,
+                    double* total_ms);
 
 /* ------------------------------------------------------------- tensors */
 

@@ -1,6 +1,7 @@
 // extern "C" entry points of include/sdu.h.  Every function validates its
 // arguments, returns a status code and never lets an exception cross the ABI.
 #include "engine.h"
+#include "graph.h"
 
 #include <cmath>
 #include <cstdint>
@@ -65,6 +66,35 @@ bool gemm_output_aliases(const sdu_tensor* y, size_t yb, const sdu_tensor* a, si
     const bool res_in_place = !out_f32 && res && dptr(res) == dptr(y);
     return overlaps(y, yb, a, ab) || overlaps(y, yb, a2, a2b) || overlaps(y, yb, w, wb) ||
            overlaps(y, yb, bias, bb) || (res && !res_in_place && overlaps(y, yb, res, rb));
+}
+
+// While op-level timing is on (sdu_profile_ops), the kernels an op-level call launches
+// go through the context's event timer, each with its own start / stop events, under the
+// op's name.
+struct OpTimerScope {
+    KernelTimer* prev;
+    bool on;
+    OpTimerScope(sdu_ctx* ctx, const char* op) : prev(g_kernel_timer), on(ctx && ctx->op_timer) {
+        if (!on) return;
+        EventTimer* t = (EventTimer*)ctx->op_timer;
+        t->cat = op;
+        t->shape.clear();
+        g_kernel_timer = t;
+    }
+    ~OpTimerScope() {
+        if (on) g_kernel_timer = prev;
+    }
+};
+
+void drop_op_timer(sdu_ctx* ctx) {
+    EventTimer* t = (EventTimer*)ctx->op_timer;
+    if (!t) return;
+    for (ProfRec& r : t->recs) {
+        hipEventDestroy(r.e0);
+        hipEventDestroy(r.e1);
+    }
+    delete t;
+    ctx->op_timer = nullptr;
 }
 
 int finish(sdu_ctx* ctx, hipError_t e, const char* what) {
@@ -177,6 +207,7 @@ int sdu_release(sdu_ctx* ctx) {
     if (!ctx) return SDU_OK;
     Ctx& c = ctx->c;
     hipStreamSynchronize(c.stream);
+    drop_op_timer(ctx);
     free_fwd_states(c);
     aux_free(c.taesd);
     aux_free(c.clip);
@@ -587,6 +618,57 @@ int sdu_profile(sdu_ctx* ctx, int B, int H, int W, int L, sdu_prof_entry* out, i
     });
 }
 
+int sdu_profile_ops(sdu_ctx* ctx, int enable, sdu_prof_entry* out, int max_entries, int* n_entries,
+                    double* total_ms) {
+    SDU_GUARD(ctx);
+    return guarded(ctx, [&]() -> int {
+        if (n_entries) *n_entries = 0;
+        if (total_ms) *total_ms = 0.0;
+        if (enable) {
+            drop_op_timer(ctx);  // a new window
+            EventTimer* t = new EventTimer();
+            t->s = ctx->c.stream;
+            ctx->op_timer = t;
+            return SDU_OK;
+        }
+        EventTimer* t = (EventTimer*)ctx->op_timer;
+        if (!t) return fail(ctx, SDU_ERR_ARG, "op timing is not on");
+        hipError_t e = hipStreamSynchronize(ctx->c.stream);
+        std::map<std::string, ProfAcc> acc;
+        for (ProfRec& r : t->recs) {
+            float ms = 0.f;
+            if (e == hipSuccess) e = hipEventElapsedTime(&ms, r.e0, r.e1);
+            for (const std::string& key : {r.cat, std::string("k:") + r.kern}) {
+                ProfAcc& a = acc[key];
+                a.calls += 1;
+                a.ms += ms;
+                a.flops += r.flops;
+                a.bytes += r.bytes;
+            }
+        }
+        drop_op_timer(ctx);
+        if (e != hipSuccess) return hipfail(ctx, e, "profile_ops");
+        int n = 0;
+        double tot = 0;
+        for (auto& kv : acc) {
+            if (kv.first.rfind("k:", 0) != 0) tot += kv.second.ms;
+            if (out && n < max_entries) {
+                sdu_prof_entry& en = out[n];
+                memset(&en, 0, sizeof en);
+                snprintf(en.name, sizeof en.name, "%s", kv.first.c_str());
+                en.calls = kv.second.calls;
+                en.ms = kv.second.ms;
+                en.flops = kv.second.flops;
+                en.bytes = kv.second.bytes;
+            }
+            ++n;
+        }
+        if (n_entries) *n_entries = n;
+        if (total_ms) *total_ms = tot;
+        return SDU_OK;
+    });
+}
+
 // ---------------------------------------------------------------- tensors
 
 int sdu_tensor_alloc(sdu_ctx* ctx, int dtype, int ndim, const int64_t* shape, sdu_tensor** out) {
@@ -647,6 +729,7 @@ int sdu_groupnorm(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* x2, const
                   const sdu_tensor* beta, sdu_tensor* y, int B, int HW, int C1, int C2, int groups,
                   float eps, int silu) {
     SDU_GUARD(ctx);
+    OpTimerScope ots(ctx, "groupnorm");
     int st = gn_check(ctx, x, x2, gamma, beta, y, B, HW, C1, C2, groups);
     if (st) return st;
     const size_t acc = groupnorm_acc_bytes(B, groups);
@@ -664,6 +747,7 @@ int sdu_groupnorm_noalloc(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* x
                           const sdu_tensor* beta, sdu_tensor* y, int B, int HW, int C1, int C2, int groups,
                           float eps, int silu) {
     SDU_GUARD(ctx);
+    OpTimerScope ots(ctx, "groupnorm_noalloc");
     int st = gn_check(ctx, x, x2, gamma, beta, y, B, HW, C1, C2, groups);
     if (st) return st;
     const size_t acc = groupnorm_acc_bytes(B, groups);
@@ -683,6 +767,7 @@ int sdu_groupnorm_noalloc(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* x
 int sdu_layernorm(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* gamma, const sdu_tensor* beta,
                   sdu_tensor* y, int T, int C, float eps) {
     SDU_GUARD(ctx);
+    OpTimerScope ots(ctx, "layernorm");
     if (T < 1 || C < 8 || C % 8 || C > 2048) return fail(ctx, SDU_ERR_ARG, "bad layernorm shape");
     if (!fits(x, (size_t)T * C * 2) || !fits(y, (size_t)T * C * 2) || !fits(gamma, (size_t)C * 2) ||
         !fits(beta, (size_t)C * 2))
@@ -696,6 +781,7 @@ int sdu_matmul(sdu_ctx* ctx, const sdu_tensor* a, const sdu_tensor* a2, const sd
                const sdu_tensor* bias, const sdu_tensor* residual, sdu_tensor* y, int M, int N, int K,
                int K2, int flags) {
     SDU_GUARD(ctx);
+    OpTimerScope ots(ctx, "matmul");
     const int geglu = (flags & SDU_EPI_GEGLU) != 0;
     const int f32 = (flags & SDU_EPI_OUT_F32) != 0;
     const int K1 = K - K2;
@@ -730,6 +816,7 @@ int sdu_conv2d(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* w, const sdu
                const sdu_tensor* temb, const sdu_tensor* residual, sdu_tensor* y, int B, int H, int W,
                int Ci, int Co, int ksize, int stride, int upsample, int flags) {
     SDU_GUARD(ctx);
+    OpTimerScope ots(ctx, "conv2d");
     const int f32 = (flags & SDU_EPI_OUT_F32) != 0;
     if (B < 1 || H < 1 || W < 1 || Ci < 8 || Ci % 8 || Co < 1 || (ksize != 1 && ksize != 3) ||
         (stride != 1 && stride != 2) || (upsample && stride != 1) || (ksize == 1 && (stride != 1 || upsample)) ||
@@ -776,6 +863,7 @@ int sdu_conv2d_groupnorm(sdu_ctx* ctx, const sdu_tensor* x, const sdu_tensor* w,
                          const sdu_tensor* gamma, const sdu_tensor* beta, sdu_tensor* gn_y, int B, int H,
                          int W, int Ci, int Co, int groups, float eps, int silu) {
     SDU_GUARD(ctx);
+    OpTimerScope ots(ctx, "conv2d_groupnorm");
     const int HW = H * W;
     if (B < 1 || B > 64 || H < 1 || W < 1 || Ci < 8 || Ci % 8 || Co < 8 || Co % 8 || Co > 2560 || groups < 1 ||
         groups > 32 || Co % groups || HW < 64 || !gemm_stats_supported(HW) || !(eps > 0.f))
@@ -838,6 +926,7 @@ int sdu_attention_ex(sdu_ctx* ctx, const sdu_tensor* q, const sdu_tensor* k, con
                      sdu_tensor* o, int B, int heads, int Sq, int Sk, int d, int ldq, int ldk, int ldv,
                      int ldo, float scale, int flags) {
     SDU_GUARD(ctx);
+    OpTimerScope ots(ctx, "attention");
     const int causal = (flags & SDU_ATTN_CAUSAL) != 0;
     if ((flags & ~SDU_ATTN_CAUSAL) || (causal && Sq != Sk)) return fail(ctx, SDU_ERR_ARG, "bad attention flags");
     if (B < 1 || heads < 1 || Sq < 1 || Sk < 1 || d < 8 || d > 160 || d % 8 || ldq < heads * d ||
@@ -854,6 +943,7 @@ int sdu_attention_ex(sdu_ctx* ctx, const sdu_tensor* q, const sdu_tensor* k, con
 
 int sdu_geglu(sdu_ctx* ctx, const sdu_tensor* g, sdu_tensor* y, int T, int C2) {
     SDU_GUARD(ctx);
+    OpTimerScope ots(ctx, "geglu");
     if (T < 1 || C2 < 1) return fail(ctx, SDU_ERR_ARG, "bad geglu shape");
     if (!fits(g, (size_t)T * C2 * 4) || !fits(y, (size_t)T * C2 * 2)) return fail(ctx, SDU_ERR_ARG, "geglu tensor too small");
     return finish(ctx, geglu_launch((const f16*)dptr(g), (f16*)dptr(y), T, C2, ctx->c.stream), "geglu");
@@ -861,6 +951,7 @@ int sdu_geglu(sdu_ctx* ctx, const sdu_tensor* g, sdu_tensor* y, int T, int C2) {
 
 int sdu_silu(sdu_ctx* ctx, const sdu_tensor* x, sdu_tensor* y, int64_t n) {
     SDU_GUARD(ctx);
+    OpTimerScope ots(ctx, "silu");
     if (n < 0 || !fits(x, (size_t)n * 2) || !fits(y, (size_t)n * 2)) return fail(ctx, SDU_ERR_ARG, "bad silu");
     if (n == 0) return SDU_OK;
     return finish(ctx, silu_launch((const f16*)dptr(x), (f16*)dptr(y), n, ctx->c.stream), "silu");
@@ -868,6 +959,7 @@ int sdu_silu(sdu_ctx* ctx, const sdu_tensor* x, sdu_tensor* y, int64_t n) {
 
 int sdu_add(sdu_ctx* ctx, const sdu_tensor* a, const sdu_tensor* b, sdu_tensor* y, int64_t n) {
     SDU_GUARD(ctx);
+    OpTimerScope ots(ctx, "add");
     if (n < 0 || !fits(a, (size_t)n * 2) || !fits(b, (size_t)n * 2) || !fits(y, (size_t)n * 2))
         return fail(ctx, SDU_ERR_ARG, "bad add");
     if (n == 0) return SDU_OK;
@@ -876,6 +968,7 @@ int sdu_add(sdu_ctx* ctx, const sdu_tensor* a, const sdu_tensor* b, sdu_tensor* 
 
 int sdu_add_bias(sdu_ctx* ctx, sdu_tensor* y, const sdu_tensor* bias, int64_t n, int C) {
     SDU_GUARD(ctx);
+    OpTimerScope ots(ctx, "add_bias");
     if (n < 0 || C < 1 || !fits(y, (size_t)n * 2) || !fits(bias, (size_t)C * 2))
         return fail(ctx, SDU_ERR_ARG, "bad add_bias");
     if (n == 0) return SDU_OK;
@@ -885,6 +978,7 @@ int sdu_add_bias(sdu_ctx* ctx, sdu_tensor* y, const sdu_tensor* bias, int64_t n,
 int sdu_lcm_step(sdu_ctx* ctx, sdu_tensor* x, const sdu_tensor* eps2, const sdu_tensor* noise, int64_t n,
                  int steps, int idx, float guidance) {
     SDU_GUARD(ctx);
+    OpTimerScope ots(ctx, "lcm_step");
     if (n < 1 || steps < 1 || steps > 50 || idx < 0 || idx >= steps) return fail(ctx, SDU_ERR_ARG, "bad lcm step");
     const bool last = idx == steps - 1;
     if (!fits(x, (size_t)n * 4) || !fits(eps2, (size_t)2 * n * 4) || (!last && !fits(noise, (size_t)n * 4)))

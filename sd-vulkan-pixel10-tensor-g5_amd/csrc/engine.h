@@ -208,6 +208,8 @@ void free_fwd_states(Ctx& c);
 
 struct sdu_ctx {
     sdu::Ctx c;
+    // op-level kernel timing (sdu_profile_ops): an EventTimer of graph.h while enabled
+    void* op_timer = nullptr;
 };
 struct sdu_tensor {
     sdu::sdu_tensor_impl t;

@@ -1237,22 +1237,22 @@ hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s) {
         return hipErrorInvalidValue;
     dim3 grid(ceil_div(a.M, g.mt) * ceil_div(a.N, g.nt), 1, splits);
     // algorithmic traffic: A once (the conv source image, not its im2col), W once, output
-    // (+ residual) once; a split pays its fp32 partials out and back
+    // (+ residual) once.  A split's fp32 partials are overhead, not algorithmic traffic:
+    // they are counted nowhere, and the reduce launch reports no algorithmic bytes
     const int nout = a.geglu ? a.N / 2 : a.N;
     const double a_bytes = a.amode == A_CONV3 ? 2.0 * a.Bn * a.Hin * a.Win * a.Cin + 2.0 * a.M * (a.K - a.K1)
                                               : 2.0 * a.M * a.K;
     const double out_bytes = (double)a.M * nout * (a.out_mode == OUT_F16 ? 2.0 : 4.0) +
                              (a.res ? 2.0 * a.M * nout : 0.0);
-    const double part_bytes = splits > 1 ? 4.0 * splits * a.M * a.N : 0.0;
     const double flops = 2.0 * a.M * a.N * a.K;
-    const double k_bytes = a_bytes + 2.0 * a.N * a.K + (fix ? 2.0 * part_bytes + out_bytes : splits > 1 ? part_bytes : out_bytes);
+    const double k_bytes = a_bytes + 2.0 * a.N * a.K + out_bytes;
     launch_timed(kNames[ci][a.amode == A_CONV3], flops, k_bytes, [&] {
         if (a.amode == A_DENSE) launch_cfg<A_DENSE>(ci, grid, a, s);
         else launch_cfg<A_CONV3>(ci, grid, a, s);
     });
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || splits == 1 || fix) return e;
-    return splitk_reduce_launch(a, part_bytes + out_bytes, s);
+    return splitk_reduce_launch(a, 0.0, s);
 }
 
 hipError_t splitk_reduce_launch(const GemmArgs& a, double bytes, hipStream_t s) {

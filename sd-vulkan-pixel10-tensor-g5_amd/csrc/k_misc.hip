@@ -137,13 +137,48 @@ __device__ __forceinline__ f16 f16_via_f32(float f) {
     return (f16)f;
 }
 
+// Elementwise ops over n fp16 values: 8 per thread with 16-byte loads and stores when
+// every pointer is 16-byte aligned, one per thread otherwise.
+template <bool V8>
 __global__ void silu_kernel(const f16* x, f16* y, int64_t n) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) y[i] = (f16)silu_f((float)x[i]);
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (V8) {
+        const int64_t i = t * 8;
+        if (i + 8 <= n) {
+            const uint4 v = *(const uint4*)(x + i);
+            const f16* h = (const f16*)&v;
+            uint4 o;
+            f16* oh = (f16*)&o;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) oh[e] = (f16)silu_f((float)h[e]);
+            *(uint4*)(y + i) = o;
+        } else {
+            for (int64_t j = i; j < n; ++j) y[j] = (f16)silu_f((float)x[j]);
+        }
+    } else if (t < n) {
+        y[t] = (f16)silu_f((float)x[t]);
+    }
 }
+template <bool V8>
 __global__ void add_kernel(const f16* a, const f16* b, f16* y, int64_t n) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) y[i] = (f16)((float)a[i] + (float)b[i]);
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (V8) {
+        const int64_t i = t * 8;
+        if (i + 8 <= n) {
+            const uint4 u = *(const uint4*)(a + i), v = *(const uint4*)(b + i);
+            const f16* ha = (const f16*)&u;
+            const f16* hb = (const f16*)&v;
+            uint4 o;
+            f16* oh = (f16*)&o;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) oh[e] = (f16)((float)ha[e] + (float)hb[e]);
+            *(uint4*)(y + i) = o;
+        } else {
+            for (int64_t j = i; j < n; ++j) y[j] = (f16)((float)a[j] + (float)b[j]);
+        }
+    } else if (t < n) {
+        y[t] = (f16)((float)a[t] + (float)b[t]);
+    }
 }
 __global__ void add_bias_kernel(f16* y, const f16* bias, int64_t n, int C) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -158,12 +193,24 @@ __global__ void geglu_kernel(const f16* g, f16* y, int T, int C2) {
     y[i] = (f16)(a * gelu_erf(bb));
 }
 
+static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
 hipError_t silu_launch(const f16* x, f16* y, int64_t n, hipStream_t s) {
-    SDU_LAUNCH(silu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, y, n);
+    const bool v8 = al16(x) && al16(y);
+    const int64_t th = v8 ? (n + 7) / 8 : n;
+    launch_timed(v8 ? "silu_kernel<1>" : "silu_kernel<0>", 0.0, 4.0 * n, [&] {
+        if (v8) SDU_LAUNCH(silu_kernel<true>, dim3((unsigned)((th + 255) / 256)), dim3(256), 0, s, x, y, n);
+        else SDU_LAUNCH(silu_kernel<false>, dim3((unsigned)((th + 255) / 256)), dim3(256), 0, s, x, y, n);
+    });
     return hipGetLastError();
 }
 hipError_t add_launch(const f16* a, const f16* b, f16* y, int64_t n, hipStream_t s) {
-    SDU_LAUNCH(add_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a, b, y, n);
+    const bool v8 = al16(a) && al16(b) && al16(y);
+    const int64_t th = v8 ? (n + 7) / 8 : n;
+    launch_timed(v8 ? "add_kernel<1>" : "add_kernel<0>", 0.0, 6.0 * n, [&] {
+        if (v8) SDU_LAUNCH(add_kernel<true>, dim3((unsigned)((th + 255) / 256)), dim3(256), 0, s, a, b, y, n);
+        else SDU_LAUNCH(add_kernel<false>, dim3((unsigned)((th + 255) / 256)), dim3(256), 0, s, a, b, y, n);
+    });
     return hipGetLastError();
 }
 hipError_t add_bias_launch(f16* y, const f16* bias, int64_t n, int C, hipStream_t s) {

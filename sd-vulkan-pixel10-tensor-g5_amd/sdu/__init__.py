@@ -39,7 +39,7 @@ SDU_ATTN_CAUSAL = 0x1
 EXPORTS = [
     "sdu_init", "sdu_release", "sdu_last_error", "sdu_synchronize", "sdu_set_weight",
     "sdu_get_weight", "sdu_param_count", "sdu_forward", "sdu_forward_cfg", "sdu_denoise_lcm",
-    "sdu_forward_device", "sdu_denoise_lcm_device", "sdu_denoise_lcm_ex", "sdu_selftest", "sdu_selftest_ex", "sdu_time_proj", "sdu_profile",
+    "sdu_forward_device", "sdu_denoise_lcm_device", "sdu_denoise_lcm_ex", "sdu_selftest", "sdu_selftest_ex", "sdu_time_proj", "sdu_profile", "sdu_profile_ops",
     "sdu_tensor_alloc", "sdu_tensor_free", "sdu_tensor_upload", "sdu_tensor_download",
     "sdu_tensor_device_ptr", "sdu_tensor_bytes", "sdu_groupnorm", "sdu_groupnorm_noalloc", "sdu_layernorm", "sdu_matmul",
     "sdu_conv2d", "sdu_conv2d_groupnorm", "sdu_attention", "sdu_attention_ex", "sdu_geglu", "sdu_silu", "sdu_add", "sdu_add_bias",
@@ -105,6 +105,7 @@ def load(path: str = LIB_PATH):
         "sdu_selftest_ex": ([P, ctypes.c_char_p, ctypes.POINTER(SelftestReport)], I),
         "sdu_time_proj": ([I, P], I),
         "sdu_profile": ([P, I, I, I, I, P, I, ctypes.POINTER(I), ctypes.POINTER(ctypes.c_double)], I),
+        "sdu_profile_ops": ([P, I, P, I, ctypes.POINTER(I), ctypes.POINTER(ctypes.c_double)], I),
         "sdu_tensor_alloc": ([P, I, I, ctypes.POINTER(I64), ctypes.POINTER(P)], I),
         "sdu_tensor_free": ([P, P], I),
         "sdu_tensor_upload": ([P, P, P, SZ], I),
@@ -304,6 +305,21 @@ class Engine:
                                        ctypes.byref(tot)))
         out = {}
         for i in range(min(n.value, 128)):
+            e = arr[i]
+            out[e.name.decode()] = dict(calls=e.calls, ms=e.ms, flops=e.flops, bytes=e.bytes)
+        return out, tot.value
+
+    def profile_ops(self, enable: bool):
+        """sdu_profile_ops: enable=True opens a kernel-timing window over op-level calls;
+        enable=False closes it and returns ({name: calls/ms/flops/bytes}, total_ms)."""
+        if enable:
+            self._check(load().sdu_profile_ops(self.h, 1, None, 0, None, None))
+            return None
+        arr = (ProfEntry * 256)()
+        n, tot = I(), ctypes.c_double()
+        self._check(load().sdu_profile_ops(self.h, 0, arr, 256, ctypes.byref(n), ctypes.byref(tot)))
+        out = {}
+        for i in range(min(n.value, 256)):
             e = arr[i]
             out[e.name.decode()] = dict(calls=e.calls, ms=e.ms, flops=e.flops, bytes=e.bytes)
         return out, tot.value

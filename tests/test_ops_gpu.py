@@ -433,9 +433,10 @@ def test_attention_strided_rows(op_engine):
 # ------------------------------------------------------------------ elementwise
 
 
-def test_elementwise_ops(op_engine):
+@pytest.mark.parametrize("n", [3000, 1003, 5])  # 8-wide vectors; a 3-element tail; tail only
+def test_elementwise_ops(op_engine, n):
     e = op_engine
-    n, C = 3 * 1000, 40
+    C = 40 if n % 40 == 0 else 1
     x = r16((n,), 20, 3.0)
     y = r16((n,), 21)
     b = r16((C,), 22)
