@@ -394,6 +394,10 @@ def test_conv2d_inplace_residual_and_overlap_errors(op_engine):
     (2, 8, 2050, 1030, 40),   # 128-key tiles (at most 512 blocks)
     (4, 8, 4000, 333, 40),    # 64-key tiles
     (4, 8, 1000, 700, 80),    # eight query waves per block
+    # many shared-tile blocks (more than one round): ragged query count (last block with
+    # 4 queries) and key count (last 64-key tile with 13)
+    (8, 8, 4100, 333, 40),
+    (4, 16, 2048, 200, 40),
 ])
 def test_attention(op_engine, B, heads, Sq, Sk, d):
     say(f"attention B={B} heads={heads} Sq={Sq} Sk={Sk} d={d}")
