@@ -50,6 +50,12 @@ struct Exec {
     double* gn_acc = nullptr;  // next free GroupNorm accumulator slot (zeroed per forward)
     double* st_next = nullptr;  // per-channel output statistics pool (zeroed per forward)
     double* st_end = nullptr;
+    // A forward clears its statistics pool in the launch that stages its inputs, outside
+    // the graph (stats_outside): the pool's address and size are recorded here instead of
+    // a fill kernel being captured.
+    bool stats_outside = false;
+    void* stats_pool = nullptr;
+    size_t stats_bytes = 0;
     hipError_t err = hipSuccess;
     EventTimer* timer = nullptr;  // eager profiling only
 

@@ -965,6 +965,7 @@ void gemm_kernel(GemmArgs a) {
 constexpr int kNarrowPix = 16, kNarrowSlices = 16, kNarrowBatch = 12;
 template <int CO>
 __global__ __launch_bounds__(256) void conv3_narrow_kernel(GemmArgs a) {
+    if (a.c_ind) a.C = *a.c_ind;
     typedef _Float16 half2v __attribute__((ext_vector_type(2)));
     extern __shared__ uint4 wsm[];  // [CO][nchunk]
     const int cpt = a.Cin / 8, nchunk = 9 * cpt;
@@ -1192,6 +1193,7 @@ hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s) {
         });
         return hipGetLastError();
     }
+    if (a.c_ind) return hipErrorInvalidValue;  // the narrow conv only
     int ci, splits, kps;
     bool fix;
     plan(a, ci, splits, kps, fix);

@@ -41,10 +41,13 @@ hipError_t nchw_to_nhwc_launch(const float* src, f16* dst, int B, int Bsrc, int 
 // The UNet forward's inputs in one launch, outside its graph: the latent NCHW fp32
 // [B,C,H,W] -> NHWC fp16 [B,H,W,Cpad] (channels >= C zero), the context fp32 -> fp16,
 // and ntemb floats of the time projection copied.  Threads [0, nlat) take the latent,
-// the next nctx the context, the next ntemb the time projection.
+// the next nctx the context, the next ntemb the time projection, the next nzero16 clear
+// 16-byte words at zero_dst; thread 0 also stores out_ptr to *out_slot (when set).
 __global__ void stage_in_kernel(const float* lat, const float* ctx, const float* temb, f16* lat16, f16* ctx16,
-                                float* temb_dst, int B, int C, int Cpad, int HW, int64_t nctx, int ntemb) {
+                                float* temb_dst, int B, int C, int Cpad, int HW, int64_t nctx, int ntemb,
+                                uint4* zero_dst, int64_t nzero16, void** out_slot, void* out_ptr) {
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i == 0 && out_slot) *out_slot = out_ptr;
     const int64_t nlat = (int64_t)B * HW * Cpad;
     if (i < nlat) {
         const int c = (int)(i % Cpad);
@@ -59,16 +62,22 @@ __global__ void stage_in_kernel(const float* lat, const float* ctx, const float*
         return;
     }
     i -= nctx;
-    if (i < ntemb) temb_dst[i] = temb[i];
+    if (i < ntemb) {
+        temb_dst[i] = temb[i];
+        return;
+    }
+    i -= ntemb;
+    if (i < nzero16) zero_dst[i] = make_uint4(0, 0, 0, 0);
 }
 
 hipError_t stage_in_launch(const float* lat, const float* ctx, const float* temb, f16* lat16, f16* ctx16,
                            float* temb_dst, int B, int C, int Cpad, int HW, int64_t nctx, int ntemb,
-                           hipStream_t s) {
-    const int64_t nlat = (int64_t)B * HW * Cpad, total = nlat + nctx + ntemb;
-    launch_timed("stage_in_kernel", 0.0, 4.0 * B * C * HW + 2.0 * nlat + 6.0 * nctx + 8.0 * ntemb, [&] {
+                           hipStream_t s, void* zero_dst, size_t zero_bytes, void** out_slot, void* out_ptr) {
+    const int64_t nlat = (int64_t)B * HW * Cpad, nz = (int64_t)((zero_bytes + 15) / 16);
+    const int64_t total = nlat + nctx + ntemb + nz;
+    launch_timed("stage_in_kernel", 0.0, 4.0 * B * C * HW + 2.0 * nlat + 6.0 * nctx + 8.0 * ntemb + 16.0 * nz, [&] {
         SDU_LAUNCH(stage_in_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, lat, ctx, temb, lat16,
-                   ctx16, temb_dst, B, C, Cpad, HW, nctx, ntemb);
+                   ctx16, temb_dst, B, C, Cpad, HW, nctx, ntemb, (uint4*)zero_dst, nz, out_slot, out_ptr);
     });
     return hipGetLastError();
 }

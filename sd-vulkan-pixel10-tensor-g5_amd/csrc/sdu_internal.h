@@ -99,6 +99,10 @@ struct GemmArgs {
     void* C;            // output
     int ldc;            // row stride of C in elements (after GEGLU: N/2 columns)
     int out_mode;
+    // when set (the narrow-output conv only): the output pointer is read from this device
+    // word at launch time instead of C, so a captured graph can write to a buffer that
+    // changes between replays
+    void* const* c_ind;
     int hw_out;         // OUT_F32_NCHW: pixels per image
     int geglu;
     int act;            // activation on the final value (after bias, GEGLU, residual): ACT_*
@@ -190,10 +194,12 @@ hipError_t nchw_to_nhwc_launch(const float* src, f16* dst, int B, int Bsrc, int 
                                hipStream_t s, int tanh_clamp = 0);
 // The UNet forward's inputs in one launch: latent NCHW fp32 [B,C,H,W] -> NHWC fp16
 // [B,H,W,Cpad], context fp32 -> fp16 (nctx values), ntemb time-projection floats copied
-// to temb_dst (ntemb 0: none).
+// to temb_dst (ntemb 0: none).  The same launch clears zero_bytes (rounded up to 16) at
+// the 16-byte aligned zero_dst and, when out_slot is set, stores out_ptr there.
 hipError_t stage_in_launch(const float* lat, const float* ctx, const float* temb, f16* lat16, f16* ctx16,
                            float* temb_dst, int B, int C, int Cpad, int HW, int64_t nctx, int ntemb,
-                           hipStream_t s);
+                           hipStream_t s, void* zero_dst = nullptr, size_t zero_bytes = 0,
+                           void** out_slot = nullptr, void* out_ptr = nullptr);
 // Token + position embedding: out[b*S + i][:] = tok[ids[b*S + i]][:] + pos[i][:] (fp16,
 // summed in fp32), ids clamped to [0, vocab).  C % 8 == 0.
 hipError_t embed_launch(const int32_t* ids, const f16* tok, const f16* pos, f16* out, int B, int S, int C,

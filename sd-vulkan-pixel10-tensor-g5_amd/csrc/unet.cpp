@@ -252,8 +252,10 @@ static f16* cross_kv(Exec& E, const f16* ctx16, int L) {
 // UNet body: lat NHWC fp16 [B,H,W,8] -> eps fp32 NCHW [B,4,H,W] (vk_engine.cpp:711-790).
 // tproj_pre: the time projections of this forward when already computed (a denoise
 // computes every step's at once); otherwise they are formed here from temb320.
+// out_ind: when set, conv_out reads its output pointer from this device word (written
+// before each replay) instead of writing to `out`.
 static void unet_core(Exec& E, const Fwd& F, const f16* lat, const float* temb320, const f16* kv,
-                      float* out, const float* tproj_pre = nullptr) {
+                      float* out, const float* tproj_pre = nullptr, void* const* out_ind = nullptr) {
     Ctx& c = E.c;
     const size_t mk0 = E.ar->mark();
     // GroupNorm accumulators of this forward (2 per resnet, 1 per transformer, conv_norm_out)
@@ -270,7 +272,10 @@ static void unet_core(Exec& E, const Fwd& F, const f16* lat, const float* temb32
     E.gn_acc = E.alloc<double>(acc_n + st_n);
     E.st_next = E.gn_acc + acc_n;
     E.st_end = E.st_next + st_n;
-    {
+    if (E.stats_outside) {
+        E.stats_pool = E.gn_acc;
+        E.stats_bytes = (acc_n + st_n) * sizeof(double);
+    } else {
         void* p = E.gn_acc;
         E.run("groupnorm", [&] { return zero_launch(p, (acc_n + st_n) * sizeof(double), E.s); });
     }
@@ -334,6 +339,7 @@ static void unet_core(Exec& E, const Fwd& F, const f16* lat, const float* temb32
     a.out_mode = OUT_F32_NCHW;
     a.ldc = kLatC;
     a.hw_out = H * Wd;
+    a.c_ind = out_ind;
     gemm(E, "conv3x3", a);
     E.ar->release(mk0);
 }
@@ -411,6 +417,11 @@ struct FwdState {
     // stage_in launch from the caller's buffers
     f16* lat16 = nullptr;      // [B,H,W,8]
     f16* ctx16 = nullptr;      // [B,L,768]
+    // forward: the statistics pool the staging launch clears before each replay, and the
+    // device word holding the output pointer that conv_out reads (set by that launch)
+    void* stats_pool = nullptr;
+    size_t stats_bytes = 0;
+    void** out_slot = nullptr;
     hipGraphExec_t exec = nullptr;
 };
 
@@ -423,7 +434,15 @@ static void body(Exec& E, FwdState& S) {
         S.lat16 = E.alloc<f16>((size_t)F.B * HW * kLatCpad);
         S.ctx16 = E.alloc<f16>((size_t)F.B * F.L * kCtxDim);
         const f16* kv = cross_kv(E, S.ctx16, F.L);
-        unet_core(E, F, S.lat16, S.in_temb, kv, S.out);
+        // the graph: statistics cleared and output pointer set by the staging launch
+        // before each replay; the eager profiling pass clears them itself and writes to
+        // the state's own output
+        E.stats_outside = E.timer == nullptr;
+        unet_core(E, F, S.lat16, S.in_temb, kv, S.out, nullptr, E.timer ? nullptr : S.out_slot);
+        if (E.stats_outside) {
+            S.stats_pool = E.stats_pool;
+            S.stats_bytes = E.stats_bytes;
+        }
         return;
     }
     // denoise: x (fp32 [4,H,W]) lives in `out`; B = 2 (cond, uncond)
@@ -472,6 +491,7 @@ static void free_state(FwdState* S) {
     hipFree(S->in_noise);
     hipFree(S->out);
     hipFree(S->d_guidance);
+    hipFree(S->out_slot);
 }
 
 void free_fwd_states(Ctx& c) {
@@ -508,6 +528,8 @@ static int plan_state(Ctx& c, FwdState& S) {
         return set_err(&c, SDU_ERR_OOM, "staging");
     if ((e = mal((void**)&S.out, lat_n * 4)) != hipSuccess) return set_err(&c, SDU_ERR_OOM, "staging");
     if (S.kind == 1 && (e = mal((void**)&S.d_guidance, 4)) != hipSuccess) return set_err(&c, SDU_ERR_OOM, "staging");
+    if (S.kind == 0 && (e = mal((void**)&S.out_slot, sizeof(void*))) != hipSuccess)
+        return set_err(&c, SDU_ERR_OOM, "staging");
     if (S.kind == 1) {
         LcmSched sched(S.steps);
         std::vector<float> te((size_t)S.steps * 320);
@@ -576,11 +598,14 @@ static int check_shape(Ctx& c, int B, int H, int W, int L) {
 }
 
 // A forward state's inputs into its graph's fp16 buffers, in one launch (temb NULL: the
-// time projection is already in S.in_temb).
-static hipError_t stage_inputs(Ctx& c, const FwdState& S, const float* lat, const float* temb, const float* ctx) {
+// time projection is already in S.in_temb), which also clears the forward's statistics
+// pool and points the graph's output at `out`.
+static hipError_t stage_inputs(Ctx& c, const FwdState& S, const float* lat, const float* temb, const float* ctx,
+                               float* out) {
     const Fwd& F = S.f;
     return stage_in_launch(lat, ctx, temb, S.lat16, S.ctx16, S.in_temb, F.B, kLatC, kLatCpad, F.H * F.W,
-                           (int64_t)F.B * F.L * kCtxDim, temb ? 320 : 0, c.stream);
+                           (int64_t)F.B * F.L * kCtxDim, temb ? 320 : 0, c.stream, S.stats_pool, S.stats_bytes,
+                           S.out_slot, out);
 }
 
 int unet_forward_device(Ctx& c, const float* d_lat, const float* d_temb, const float* d_ctx, int B, int H,
@@ -589,10 +614,8 @@ int unet_forward_device(Ctx& c, const float* d_lat, const float* d_temb, const f
     if (st) return st;
     FwdState* S = get_state(c, 0, B, H, W, L, 0, 0, &st);
     if (!S) return st;
-    const size_t lat_b = (size_t)B * kLatC * H * W * 4;
     hipError_t e;
-    if ((e = stage_inputs(c, *S, d_lat, d_temb, d_ctx)) || (e = hipGraphLaunch(S->exec, c.stream)) ||
-        (e = hipMemcpyAsync(d_out, S->out, lat_b, hipMemcpyDeviceToDevice, c.stream)))
+    if ((e = stage_inputs(c, *S, d_lat, d_temb, d_ctx, d_out)) || (e = hipGraphLaunch(S->exec, c.stream)))
         return hip_fail(c, e, "forward");
     return SDU_OK;
 }
@@ -608,7 +631,7 @@ int unet_forward_host(Ctx& c, const float* lat, const float* temb, const float* 
     if ((e = hipMemcpyAsync(S->in_lat, lat, lat_b, hipMemcpyHostToDevice, c.stream)) ||
         (e = hipMemcpyAsync(S->in_temb, temb, 320 * 4, hipMemcpyHostToDevice, c.stream)) ||
         (e = hipMemcpyAsync(S->in_ctx, ctx, (size_t)B * L * kCtxDim * 4, hipMemcpyHostToDevice, c.stream)) ||
-        (e = stage_inputs(c, *S, S->in_lat, nullptr, S->in_ctx)) || (e = hipGraphLaunch(S->exec, c.stream)) ||
+        (e = stage_inputs(c, *S, S->in_lat, nullptr, S->in_ctx, S->out)) || (e = hipGraphLaunch(S->exec, c.stream)) ||
         (e = hipMemcpyAsync(out, S->out, lat_b, hipMemcpyDeviceToHost, c.stream)) ||
         (e = hipStreamSynchronize(c.stream)))
         return hip_fail(c, e, "forward");
