@@ -302,8 +302,14 @@ int sdu_attention(sdu_ctx* ctx, const sdu_tensor* q, const sdu_tensor* k, const 
                   sdu_tensor* o, int B, int heads, int Sq, int Sk, int d, int ldq, int ldk,
                   int ldv, int ldo, float scale);
 /* sdu_attention with flags: SDU_ATTN_CAUSAL masks key j > query i (Sq == Sk), the causal
- * self-attention of the CLIP text encoder behind VulkanUnetPipeline.kt:48-53. */
+ * self-attention of the CLIP text encoder behind VulkanUnetPipeline.kt:48-53.
+ * SDU_ATTN_Q_LOG2 (no counterpart in the reference): q already holds q * scale * log2(e),
+ * as the UNet's query projections write it (the softmax factor folded into their
+ * weights), so o = softmax_2(q k^T) v; scale must still be > 0 and is otherwise unused.
+ * Heads whose size is not a multiple of 16 then carry the softmax's running reference in
+ * a spare MFMA dimension (one floating-point operation less per score). */
 #define SDU_ATTN_CAUSAL 0x1
+#define SDU_ATTN_Q_LOG2 0x2
 int sdu_attention_ex(sdu_ctx* ctx, const sdu_tensor* q, const sdu_tensor* k, const sdu_tensor* v,
                      sdu_tensor* o, int B, int heads, int Sq, int Sk, int d, int ldq, int ldk,
                      int ldv, int ldo, float scale, int flags);

@@ -928,7 +928,8 @@ int sdu_attention_ex(sdu_ctx* ctx, const sdu_tensor* q, const sdu_tensor* k, con
     SDU_GUARD(ctx);
     OpTimerScope ots(ctx, "attention");
     const int causal = (flags & SDU_ATTN_CAUSAL) != 0;
-    if ((flags & ~SDU_ATTN_CAUSAL) || (causal && Sq != Sk)) return fail(ctx, SDU_ERR_ARG, "bad attention flags");
+    if ((flags & ~(SDU_ATTN_CAUSAL | SDU_ATTN_Q_LOG2)) || (causal && Sq != Sk))
+        return fail(ctx, SDU_ERR_ARG, "bad attention flags");
     if (B < 1 || heads < 1 || Sq < 1 || Sk < 1 || d < 8 || d > 160 || d % 8 || ldq < heads * d ||
         ldk < heads * d || ldv < heads * d || ldo < heads * d || ldq % 8 || ldk % 8 || ldv % 8 || ldo % 8 ||
         B > 65535 || heads > 65535)
@@ -937,7 +938,7 @@ int sdu_attention_ex(sdu_ctx* ctx, const sdu_tensor* q, const sdu_tensor* k, con
         !fits(v, (size_t)B * Sk * ldv * 2) || !fits(o, (size_t)B * Sq * ldo * 2))
         return fail(ctx, SDU_ERR_ARG, "attention tensor too small");
     AttnArgs a{(const f16*)dptr(q), (const f16*)dptr(k), (const f16*)dptr(v), (f16*)dptr(o), B, heads, Sq, Sk,
-               d, ldq, ldk, ldv, ldo, scale, causal};
+               d, ldq, ldk, ldv, ldo, scale, causal, (flags & SDU_ATTN_Q_LOG2) != 0};
     return finish(ctx, attention_launch(a, ctx->c.stream), "attention");
 }
 

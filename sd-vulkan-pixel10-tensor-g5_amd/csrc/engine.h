@@ -60,6 +60,11 @@ struct ResDesc {
     f16* w2sc = nullptr;  // [cout, 9 cout + cin] = [conv2 | shortcut]
     f16* b2sc = nullptr;  // [cout] = b2 + bs
 };
+// Attention heads of every SD1.5 transformer (head size C / 8), and the factor
+// scale * log2 e = log2 e / sqrt(C / 8) that the query projections fold in.
+static const int kUnetHeads = 8;
+inline float attn_qscale(int C) { return 1.4426950408889634f / sqrtf((float)(C / kUnetHeads)); }
+
 struct XfDesc {
     std::string pf;
     int c;
@@ -69,7 +74,9 @@ struct XfDesc {
     f16* b_out = nullptr;  // [C] = Wp.bf + bp
     // LayerNorms norm1 / norm2 / norm3 folded into the GEMMs that read them (the QKV
     // projection, the cross-attention query, the GEGLU projection): fp16 W' = W.diag(gamma),
-    // fp32 bias' = b + W.beta and column sums of W' (GemmArgs::ln_colsum)
+    // fp32 bias' = b + W.beta and column sums of W' (GemmArgs::ln_colsum).  The query rows
+    // of w_qkv and all of w_q2 also carry the softmax factor attn_qscale(C): the attention
+    // reads Q in log2 units (AttnArgs::q_log2).
     f16* w_qkv = nullptr;  // [3C, C]
     f16* w_q2 = nullptr;   // [C, C]
     f16* w_ff = nullptr;   // [8C, C]

@@ -19,6 +19,10 @@
 // <= 256, exact in fp16 and far from overflow, and the O rescale is skipped on
 // almost every tile.  When the head size leaves a spare row in the last 32-row
 // dim tile, that row of V^T is set to 1 so the PV MFMA also produces the row sums.
+// When Q arrives pre-scaled by scale * log2 e (the UNet's query projections fold it
+// in) and the head size leaves a spare dimension in the last 16-wide k-step (d = 40),
+// the shared-tile kernel also moves the FMA into the MFMA: that dimension of Q holds
+// -m against a K column of ones, so the scores come out as s*c - m (ofs_update).
 //
 // Two kernels:
 //   attn_kernel       -- NWAVE query waves share each 64-key K/V tile in LDS
@@ -45,14 +49,38 @@ __device__ __forceinline__ int key_perm(int r) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Online-softmax update for NSUB 32-key sub-tiles of raw scores s (S^T layout)
-// followed by O^T += V^T . P^T.  `kvalid` = number of valid keys in the tile for this
-// lane's query (< NSUB*32 only on the last tile, or below the causal limit; may be <= 0).
-// vt: V^T tile [dim][key] with row stride vstr.
-template <int NSUB, int MTD, bool LSUM>
-__device__ __forceinline__ void softmax_pv(floatx16 (&s)[NSUB], int kvalid, float c, float& m_run,
-                                           float& l_run, floatx16 (&o)[MTD], const f16* vt, int vstr,
-                                           int hl, int lrow, int lk) {
+// P = 2^x as fp16 for the NSUB 32-key sub-tiles of scores s, x = s * c + nm (MODE 0) or
+// s (MODE 1), followed by O^T += V^T . P^T.  Returns the lane's sum of P when the row
+// sums do not come from the ones row of V^T (!LSUM).
+template <int NSUB, int MTD, bool LSUM, int MODE>
+__device__ __forceinline__ float exp_pv(const floatx16 (&s)[NSUB], float c, float nm, floatx16 (&o)[MTD],
+                                        const f16* vt, int vstr, int lrow, int lk) {
+    float psum = 0.f;
+#pragma unroll
+    for (int sub = 0; sub < NSUB; ++sub)
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            half8 pf;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float x = s[sub][st * 8 + i];
+                const float p = fast_exp2(MODE == 0 ? __builtin_fmaf(x, c, nm) : x);
+                if (!LSUM) psum += p;
+                pf[i] = (f16)p;
+            }
+            const int kofs = sub * 32 + st * 16 + lk;
+#pragma unroll
+            for (int t = 0; t < MTD; ++t) {
+                const half8 vf = *(const half8*)&vt[(t * 32 + lrow) * vstr + kofs];
+                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, o[t], 0, 0, 0);
+            }
+        }
+    return psum;
+}
+
+// Scores of keys at or past `kvalid` (tile-relative) to -inf.
+template <int NSUB>
+__device__ __forceinline__ void mask_tile(floatx16 (&s)[NSUB], int kvalid, int hl) {
     if (kvalid < NSUB * 32) {
 #pragma unroll
         for (int sub = 0; sub < NSUB; ++sub)
@@ -62,13 +90,29 @@ __device__ __forceinline__ void softmax_pv(floatx16 (&s)[NSUB], int kvalid, floa
                 if (key >= kvalid) s[sub][e] = -INFINITY;
             }
     }
+}
+
+// mask_tile, then the max over the lane's query (both halves of the wave)
+template <int NSUB>
+__device__ __forceinline__ float mask_max(floatx16 (&s)[NSUB], int kvalid, int hl) {
+    mask_tile<NSUB>(s, kvalid, hl);
     float mx = s[0][0];
 #pragma unroll
     for (int sub = 0; sub < NSUB; ++sub)
 #pragma unroll
         for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[sub][e]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float mxs = mx * c;
+    return fmaxf(mx, __shfl_xor(mx, 32));
+}
+
+// Online-softmax update for NSUB 32-key sub-tiles of raw scores s (S^T layout)
+// followed by O^T += V^T . P^T.  `kvalid` = number of valid keys in the tile for this
+// lane's query (< NSUB*32 only on the last tile, or below the causal limit; may be <= 0).
+// vt: V^T tile [dim][key] with row stride vstr.
+template <int NSUB, int MTD, bool LSUM>
+__device__ __forceinline__ void softmax_pv(floatx16 (&s)[NSUB], int kvalid, float c, float& m_run,
+                                           float& l_run, floatx16 (&o)[MTD], const f16* vt, int vstr,
+                                           int hl, int lrow, int lk) {
+    const float mxs = mask_max<NSUB>(s, kvalid, hl) * c;
     if (__ballot(mxs > m_run + kRescaleLog2)) {  // wave-uniform
         const float m_new = fmaxf(m_run, mxs);
         const float alpha = fast_exp2(m_run - m_new);  // m_run = -inf on the first tile -> 0
@@ -80,26 +124,33 @@ __device__ __forceinline__ void softmax_pv(floatx16 (&s)[NSUB], int kvalid, floa
     // (a lane whose keys so far were all masked keeps m_run = -inf: subtract 0, so that
     // its masked scores give exp2(-inf) = 0 rather than exp2(-inf + inf))
     const float nm = m_run == -INFINITY ? 0.f : -m_run;
-    float psum = 0.f;
-#pragma unroll
-    for (int sub = 0; sub < NSUB; ++sub)
-#pragma unroll
-        for (int st = 0; st < 2; ++st) {
-            half8 pf;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float p = fast_exp2(__builtin_fmaf(s[sub][st * 8 + i], c, nm));
-                if (!LSUM) psum += p;
-                pf[i] = (f16)p;
-            }
-            const int kofs = sub * 32 + st * 16 + lk;
-#pragma unroll
-            for (int t = 0; t < MTD; ++t) {
-                const half8 vf = *(const half8*)&vt[(t * 32 + lrow) * vstr + kofs];
-                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, o[t], 0, 0, 0);
-            }
-        }
+    const float psum = exp_pv<NSUB, MTD, LSUM, 0>(s, c, nm, o, vt, vstr, lrow, lk);
     if (!LSUM) l_run += psum;
+}
+
+// The softmax reference carried inside the MFMA (attn_kernel with OFS): Q holds
+// q * scale * log2 e and a spare head dimension holds -m_run against a K column of
+// ones, so the scores come out of the QK^T MFMA in log2 units already less the running
+// reference m_run, and P = 2^s costs no per-score FMA.  m_run is an fp16 value (the
+// type of the dimension that carries it), clamped to +-30000: it is set from the first
+// tile and moved whenever a tile's max exceeds it by more than 2^8; P <= 2^8 stays exact
+// in fp16 for scores below 30000 + 8 (log2 units).  Masks the tile, rescales O and the
+// row sum when the reference moves, and returns true then (wave-uniform): the caller
+// rewrites Q's spare dimension and recomputes the tile's scores.
+template <int NSUB, int MTD>
+__device__ __forceinline__ bool ofs_update(floatx16 (&s)[NSUB], int kvalid, float& m_run, float& l_run,
+                                           floatx16 (&o)[MTD], int hl, bool first) {
+    const float mx = mask_max<NSUB>(s, kvalid, hl);  // the tile's max less m_run
+    if (!__ballot(first || mx > kRescaleLog2)) return false;
+    const float m_old = first ? 0.f : m_run;  // the reference the tile's scores carry
+    float m_new = m_old + (first ? mx : fmaxf(mx, 0.f));
+    m_new = (float)(f16)fminf(fmaxf(m_new, -30000.f), 30000.f);
+    const float alpha = first ? 0.f : fast_exp2(m_old - m_new);
+#pragma unroll
+    for (int t = 0; t < MTD; ++t) o[t] *= alpha;
+    l_run *= alpha;
+    m_run = m_new;
+    return true;
 }
 
 // Row sum of P for query lrow at the end: from the ones row of V^T (LSUM: dim
@@ -129,7 +180,9 @@ __device__ __forceinline__ void vt_pad_rows(f16* vt, int vstr, int keys, int d, 
 // NWAVE: waves per block (32 queries each; they share the K/V tiles in LDS);
 // KT: keys per iteration (64, or 128 for small heads on grids of at most two blocks
 // per CU: half the barriers and per-tile softmax overhead per key).
-template <int KS, int MTD, int NWAVE, bool LSUM, int KT = 64>
+// OFS: Q holds q * scale * log2 e and head dimension d (< KS*16) carries the softmax
+// reference (ofs_update): K's column d is 1 and Q's dimension d is -m_run.
+template <int KS, int MTD, int NWAVE, bool LSUM, int KT = 64, bool OFS = false>
 __global__ __launch_bounds__(NWAVE * 64) void attn_kernel(AttnArgs a) {
     constexpr int VSTR = KT + 8;  // Vt row stride (halves)
     constexpr int NSUB = KT / 32;
@@ -143,13 +196,13 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_kernel(AttnArgs a) {
     const int d = a.d, dch = d >> 3;  // 16-byte chunks per row
     const int q0 = blockIdx.x * (NWAVE * 32) + wave * 32;
     const int lrow = lane & 31, hl = lane >> 5, lk = hl * 8;
-    const float c = a.scale * 1.4426950408889634f;
+    const float c = a.q_log2 ? 1.f : a.scale * 1.4426950408889634f;
 
-    // zero the K padding columns [d, KS*16) of both buffers and set the V^T pad rows
-    // (never overwritten by the tile stores)
+    // zero the K padding columns [d, KS*16) of both buffers (OFS: column d is 1) and set
+    // the V^T pad rows (never overwritten by the tile stores)
     for (int i = tid; i < 2 * KT; i += NTH) {
         f16* row = &Ks[i / KT][(i % KT) * KSTR];
-        for (int x = d; x < KS * 16; ++x) row[x] = (f16)0.f;
+        for (int x = d; x < KS * 16; ++x) row[x] = (f16)((OFS && x == d) ? 1.f : 0.f);
     }
     vt_pad_rows<MTD, LSUM>(Vt[0], VSTR, KT, d, tid, NTH);
     vt_pad_rows<MTD, LSUM>(Vt[1], VSTR, KT, d, tid, NTH);
@@ -265,17 +318,39 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_kernel(AttnArgs a) {
         __builtin_amdgcn_s_setprio(1);
 
         floatx16 s[NSUB];
+        auto qk = [&]() {
 #pragma unroll
-        for (int sub = 0; sub < NSUB; ++sub) {
-            s[sub] = floatx16{};
-            const f16* krow = &Ks[buf][(sub * 32 + key_perm(lrow)) * KSTR + lk];
+            for (int sub = 0; sub < NSUB; ++sub) {
+                s[sub] = floatx16{};
+                const f16* krow = &Ks[buf][(sub * 32 + key_perm(lrow)) * KSTR + lk];
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                const half8 kf = *(const half8*)(krow + ks * 16);
-                s[sub] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], s[sub], 0, 0, 0);
+                for (int ks = 0; ks < KS; ++ks) {
+                    const half8 kf = *(const half8*)(krow + ks * 16);
+                    s[sub] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], s[sub], 0, 0, 0);
+                }
             }
+        };
+        qk();
+        const int kvalid = min(KT, a.Sk - kb);
+        if constexpr (OFS) {
+            if (ofs_update<NSUB, MTD>(s, kvalid, m_run, l_run, o, hl, it == 0)) {
+                // Q's dimension d (k-step d / 16, lanes of half (d / 8) & 1, element 0)
+                // takes the new reference; the tile's scores are computed again with it
+                const f16 nr = (f16)(-m_run);
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks)
+                    if (ks == (d >> 4) && hl == ((d >> 3) & 1)) qf[ks][0] = nr;
+                // (K fragments are read from LDS again rather than kept live from the
+                // first pass across the softmax of every tile)
+                __asm__ volatile("" ::: "memory");
+                qk();
+                mask_tile<NSUB>(s, kvalid, hl);
+            }
+            const float psum = exp_pv<NSUB, MTD, LSUM, 1>(s, 1.f, 0.f, o, Vt[buf], VSTR, lrow, lk);
+            if (!LSUM) l_run += psum;
+        } else {
+            softmax_pv<NSUB, MTD, LSUM>(s, kvalid, c, m_run, l_run, o, Vt[buf], VSTR, hl, lrow, lk);
         }
-        softmax_pv<NSUB, MTD, LSUM>(s, min(KT, a.Sk - kb), c, m_run, l_run, o, Vt[buf], VSTR, hl, lrow, lk);
         __builtin_amdgcn_s_setprio(0);
         if (it + 1 < nt) store_kv(buf ^ 1);
         __syncthreads();
@@ -324,7 +399,7 @@ __global__ __launch_bounds__(NSPLIT * 64) void attn_split_kernel(AttnArgs a) {
     const int d = a.d, dch = d >> 3;
     const int q0 = blockIdx.x * 32;
     const int lrow = lane & 31, hl = lane >> 5, lk = hl * 8;
-    const float c = a.scale * 1.4426950408889634f;
+    const float c = a.q_log2 ? 1.f : a.scale * 1.4426950408889634f;
     f16* vt = (f16*)smem + wave * (MTD * 32 * VSTRS);
 
     vt_pad_rows<MTD, LSUM>(vt, VSTRS, KTS, d, lane, 64);
@@ -496,10 +571,16 @@ static void launch_cfg(const AttnArgs& a, hipStream_t s) {
         // d40 at 4096 tokens, B=2, 0.44 ms per forward against 0.46 with 64-key tiles;
         // on larger grids they lose (0.24 ms more at 9216 tokens, 0.31 ms at B=16)
         const bool kt128 = KS == 3 && nw == 4 && (long)grid.x * bh <= 512;
-        snprintf(name, sizeof name, "attn_kernel<%d,%d,%d,%d,%d>", KS, MTD, nw, (int)LSUM, kt128 ? 128 : 64);
+        // the softmax reference rides in a spare head dimension when Q is pre-scaled
+        const bool ofs = a.q_log2 && a.d < KS * 16 && nw == 4;
+        snprintf(name, sizeof name, "attn_kernel<%d,%d,%d,%d,%d%s>", KS, MTD, nw, (int)LSUM, kt128 ? 128 : 64,
+                 ofs ? ",1" : "");
+        constexpr int KTB = KS == 3 ? 128 : 64;
         launch_timed(name, flops, bytes, [&] {
             if (nw == 8) SDU_LAUNCH((attn_kernel<KS, MTD, 8, LSUM>), grid, dim3(512), 0, s, a);
-            else if (KS == 3 && kt128) SDU_LAUNCH((attn_kernel<KS, MTD, 4, LSUM, (KS == 3 ? 128 : 64)>), grid, dim3(256), 0, s, a);
+            else if (KS == 3 && kt128 && ofs) SDU_LAUNCH((attn_kernel<KS, MTD, 4, LSUM, KTB, true>), grid, dim3(256), 0, s, a);
+            else if (KS == 3 && kt128) SDU_LAUNCH((attn_kernel<KS, MTD, 4, LSUM, KTB>), grid, dim3(256), 0, s, a);
+            else if (ofs) SDU_LAUNCH((attn_kernel<KS, MTD, 4, LSUM, 64, true>), grid, dim3(256), 0, s, a);
             else SDU_LAUNCH((attn_kernel<KS, MTD, 4, LSUM>), grid, dim3(256), 0, s, a);
         });
         return;

@@ -472,12 +472,14 @@ hipError_t fold_shortcut_launch(const f16* w2, const f16* b2, const f16* ws, con
 // Wf[n, k] = fp16(gamma[k] W[n, k]), sf[n] = sum_k Wf[n, k] (of the rounded values the
 // GEMM multiplies), bf[n] = b[n] + sum_k beta[k] W[n, k].
 __global__ __launch_bounds__(256) void fold_ln_kernel(const f16* W, const f16* b, const f16* gamma,
-                                                      const f16* beta, f16* Wf, float* bf, float* sf, int K) {
+                                                      const f16* beta, f16* Wf, float* bf, float* sf, int K,
+                                                      float oscale, int nscale) {
     const int n = blockIdx.x;
+    const float cn = n < nscale ? oscale : 1.f;
     float ss = 0.f, sb = 0.f;
     for (int k = threadIdx.x; k < K; k += 256) {
         const float w = (float)W[(int64_t)n * K + k];
-        const f16 wq = (f16)(w * (float)gamma[k]);
+        const f16 wq = (f16)(w * (float)gamma[k] * cn);
         Wf[(int64_t)n * K + k] = wq;
         ss += (float)wq;
         sb += (float)beta[k] * w;
@@ -491,14 +493,14 @@ __global__ __launch_bounds__(256) void fold_ln_kernel(const f16* W, const f16* b
     __syncthreads();
     if (threadIdx.x == 0) {
         sf[n] = part[0][0] + part[0][1] + part[0][2] + part[0][3];
-        bf[n] = (b ? (float)b[n] : 0.f) + part[1][0] + part[1][1] + part[1][2] + part[1][3];
+        bf[n] = cn * ((b ? (float)b[n] : 0.f) + part[1][0] + part[1][1] + part[1][2] + part[1][3]);
     }
 }
 
 hipError_t fold_ln_launch(const f16* W, const f16* b, const f16* gamma, const f16* beta, f16* Wf, float* bf,
-                          float* sf, int N, int K, hipStream_t s) {
+                          float* sf, int N, int K, hipStream_t s, float oscale, int nscale) {
     if (N <= 0 || K <= 0) return hipErrorInvalidValue;
-    SDU_LAUNCH(fold_ln_kernel, dim3(N), dim3(256), 0, s, W, b, gamma, beta, Wf, bf, sf, K);
+    SDU_LAUNCH(fold_ln_kernel, dim3(N), dim3(256), 0, s, W, b, gamma, beta, Wf, bf, sf, K, oscale, nscale);
     return hipGetLastError();
 }
 

@@ -275,10 +275,12 @@ int fold_weights(Ctx& c, const std::string& name) {
         // to_q, to_k, to_v are consecutive [C, C] blocks of the pool: one [3C, C] weight
         if (e == hipSuccess)
             e = fold_ln_launch(c.wd(b + ".attn1.to_q.weight"), nullptr, c.wd(b + ".norm1.weight"),
-                               c.wd(b + ".norm1.bias"), xd.w_qkv, xd.b_qkv, xd.s_qkv, 3 * C, C, c.stream);
+                               c.wd(b + ".norm1.bias"), xd.w_qkv, xd.b_qkv, xd.s_qkv, 3 * C, C, c.stream,
+                               attn_qscale(C), C);
         if (e == hipSuccess)
             e = fold_ln_launch(c.wd(b + ".attn2.to_q.weight"), nullptr, c.wd(b + ".norm2.weight"),
-                               c.wd(b + ".norm2.bias"), xd.w_q2, xd.b_q2, xd.s_q2, C, C, c.stream);
+                               c.wd(b + ".norm2.bias"), xd.w_q2, xd.b_q2, xd.s_q2, C, C, c.stream,
+                               attn_qscale(C), C);
         if (e == hipSuccess)
             e = fold_ln_launch(c.wd(b + ".ff.net.0.proj.weight"), c.wd(b + ".ff.net.0.proj.bias"),
                                c.wd(b + ".norm3.weight"), c.wd(b + ".norm3.bias"), xd.w_ff, xd.b_ff, xd.s_ff,

@@ -166,6 +166,7 @@ struct AttnArgs {
     int ldq, ldk, ldv, ldo;
     float scale;
     int causal;  // query i attends keys 0..i only (Sq == Sk; the CLIP text encoder)
+    int q_log2;  // q already holds q * scale * log2 e (the projection folded it in)
 };
 hipError_t attention_launch(const AttnArgs& a, hipStream_t s);
 
@@ -246,10 +247,12 @@ hipError_t gen_launch(f16* dst, const GenDesc& g, hipStream_t s);
 hipError_t fold_ffout_launch(const f16* Wp, const f16* bp, const f16* Wf, const f16* bf, f16* wcat, f16* bcat,
                              int C, hipStream_t s);
 // LayerNorm affine folded into the Linear that reads it (init time): Wf[n, k] =
-// gamma[k] W[n, k] (fp16), bf[n] = b[n] + sum_k beta[k] W[n, k] (b may be null),
-// sf[n] = sum_k Wf[n, k] (GemmArgs::ln_colsum).
+// gamma[k] W[n, k] c_n (fp16), bf[n] = c_n (b[n] + sum_k beta[k] W[n, k]) (b may be
+// null), sf[n] = sum_k Wf[n, k] (GemmArgs::ln_colsum), with c_n = oscale for the first
+// nscale rows (an attention query projection that also applies the softmax's
+// scale * log2 e) and 1 for the others.
 hipError_t fold_ln_launch(const f16* W, const f16* b, const f16* gamma, const f16* beta, f16* Wf, float* bf,
-                          float* sf, int N, int K, hipStream_t s);
+                          float* sf, int N, int K, hipStream_t s, float oscale = 1.f, int nscale = 0);
 // Resnet shortcut fold (init time): wcat [Co, 9 Ci2 + Cs] = [conv2 (OHWI) | shortcut],
 // bcat = b2 + bs, for conv2 over Ci2 channels and a 1x1 shortcut over Cs channels.
 hipError_t fold_shortcut_launch(const f16* w2, const f16* b2, const f16* ws, const f16* bs, f16* wcat, f16* bcat,

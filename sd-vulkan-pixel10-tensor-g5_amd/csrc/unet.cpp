@@ -17,7 +17,6 @@ namespace sdu {
 
 static const int kGroups = 32;
 static const float kEps = 1e-5f;  // GN and LN (vk_engine.cpp:548-549, :652)
-static const int kHeads = 8;
 static const int kLatC = 4, kLatCpad = 8, kCtxDim = 768;
 
 // ------------------------------------------------------------------ execution
@@ -65,10 +64,11 @@ static void groupnorm(Exec& E, Act x, Act x2, int C1, int C2, const f16* g, cons
 
 static void attention(Exec& E, const char* cat, const f16* q, const f16* k, const f16* v, f16* o,
                       int Sq, int Sk, int C, int ldq, int ldk, int ldv) {
-    AttnArgs a{q, k, v, o, E.B, kHeads, Sq, Sk, C / kHeads, ldq, ldk, ldv, C,
-               1.0f / sqrtf((float)(C / kHeads))};
+    // q comes from a projection with the softmax factor folded in (attn_qscale)
+    AttnArgs a{q, k, v, o, E.B, kUnetHeads, Sq, Sk, C / kUnetHeads, ldq, ldk, ldv, C,
+               1.0f / sqrtf((float)(C / kUnetHeads)), 0, 1};
     char shape[64];
-    snprintf(shape, sizeof shape, "Sq=%d Sk=%d d=%d", Sq, Sk, C / kHeads);
+    snprintf(shape, sizeof shape, "Sq=%d Sk=%d d=%d", Sq, Sk, C / kUnetHeads);
     E.run(cat, [&] { return attention_launch(a, E.s); }, shape);
 }
 

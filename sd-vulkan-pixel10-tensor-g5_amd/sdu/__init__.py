@@ -34,6 +34,7 @@ SDU_EPI_OUT_F32 = 0x2
 SDU_EPI_RELU = 0x4
 SDU_EPI_QUICK_GELU = 0x8
 SDU_ATTN_CAUSAL = 0x1
+SDU_ATTN_Q_LOG2 = 0x2
 
 # every symbol include/sdu.h declares
 EXPORTS = [

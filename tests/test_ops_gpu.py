@@ -434,6 +434,72 @@ def test_attention_strided_rows(op_engine):
     assert rel_err_l1(got, ref) < 2e-3
 
 
+# Q pre-scaled by scale * log2 e (SDU_ATTN_Q_LOG2), as the UNet's query projections
+# write it: o = softmax_2(q k^T) v = softmax(q' k^T / sqrt(d)) v with q' = q ln2 sqrt(d).
+# Heads whose size leaves a spare MFMA dimension (8, 24, 40, 56) on the shared-tile kernel
+# carry the softmax reference in that dimension; the others only drop the scale.
+@pytest.mark.parametrize("B,heads,Sq,Sk,d", [
+    (2, 8, 4096, 4096, 40),   # UNet 64x64 self-attention: 128-key tiles
+    (2, 8, 2050, 1030, 40),   # ragged: last query block 2 queries, last key tile 6 keys
+    (8, 8, 4100, 333, 40),    # 64-key tiles, more than one round of blocks
+    (4, 8, 1100, 300, 24),    # reference dimension in the second k-step
+    (4, 8, 1100, 300, 8),     # reference dimension in the first k-step
+    (8, 8, 2048, 300, 56),    # four k-steps, dimension 56
+    (1, 2, 100, 37, 40),      # key-split kernel (no reference dimension)
+    (4, 8, 1000, 700, 80),    # eight-wave shared tiles (d a multiple of 16)
+    (2, 8, 256, 256, 160),
+])
+def test_attention_q_log2(op_engine, B, heads, Sq, Sk, d):
+    import sdu
+    say(f"attention q_log2 B={B} heads={heads} Sq={Sq} Sk={Sk} d={d}")
+    e = op_engine
+    C = heads * d
+    qs = (r16((B, Sq, C), 24) * (math.log2(math.e) / math.sqrt(d))).astype(np.float16)
+    k = r16((B, Sk, C), 25)
+    v = r16((B, Sk, C), 26)
+    tq, tk, tv = e.upload(qs), e.upload(k.astype(np.float16)), e.upload(v.astype(np.float16))
+    to = e.tensor((B, Sq, C))
+    e.attention_ex(tq, tk, tv, to, B, heads, Sq, Sk, d, C, C, C, C, 1.0 / math.sqrt(d), sdu.SDU_ATTN_Q_LOG2)
+    got = to.numpy().astype(np.float32)
+    qp = qs.astype(np.float32) * (math.log(2.0) * math.sqrt(d))
+    ref = U.attention(t(qp), t(k), t(v), heads).numpy()
+    assert rel_err_l1(got, ref) < 2e-3
+    assert np.abs(got - ref).max() < 2e-2
+
+
+@pytest.mark.parametrize("B", [4, 16])  # 128-key tiles (256 blocks), 64-key tiles (1024)
+def test_attention_q_log2_reference_moves(op_engine, B):
+    """Score offsets per key range (log2 units) that move the softmax reference carried in
+    the spare head dimension: the first tile far below zero (-3000), the next 10 higher
+    (a move of more than 2^8 on the reference), keys 400-419 at +50 (a jump of 3000),
+    the rest at +40 (no move), and a masked key tail (600 keys)."""
+    import sdu
+    say(f"attention q_log2 reference moves B={B}")
+    e = op_engine
+    heads, Sq, Sk, d = 8, 1024, 600, 40
+    C = heads * d
+    rng = np.random.default_rng(27)
+    q = (0.5 * rng.standard_normal((B, Sq, heads, d))).astype(np.float16)
+    k = (0.5 * rng.standard_normal((B, Sk, heads, d))).astype(np.float16)
+    off = np.full(Sk, 40.0)
+    off[:64] = -3000.0
+    off[64:128] = -2990.0
+    off[400:420] = 50.0
+    q[..., 0] = 8.0
+    k[..., 0] = (off / 8.0)[None, :, None]  # multiples of 1/8: exact in fp16
+    v = r16((B, Sk, C), 28)
+    q, k = q.reshape(B, Sq, C), k.reshape(B, Sk, C)
+    tq, tk, tv = e.upload(q), e.upload(k), e.upload(v.astype(np.float16))
+    to = e.tensor((B, Sq, C))
+    e.attention_ex(tq, tk, tv, to, B, heads, Sq, Sk, d, C, C, C, C, 1.0 / math.sqrt(d), sdu.SDU_ATTN_Q_LOG2)
+    got = to.numpy().astype(np.float32)
+    qp = q.astype(np.float32) * (math.log(2.0) * math.sqrt(d))
+    ref = U.attention(t(qp), t(k.astype(np.float32)), t(v), heads).numpy()
+    assert np.isfinite(got).all()
+    assert rel_err_l1(got, ref) < 2e-3
+    assert np.abs(got - ref).max() < 2e-2
+
+
 # ------------------------------------------------------------------ elementwise
 
 
