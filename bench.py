@@ -98,11 +98,28 @@ def time_forward(eng, sdu, rng, B, H, W, L, steps, warmup, mark):
     return dt / steps * 1e3, d_out
 
 
+def vae_decode_flop(H, W):
+    """SD1.5 VAE decoder work for one H x W latent: 3x3 convs as 2 * 9 * pixels * Cin * Cout,
+    the 1x1 shortcuts, the mid-block attention's four projections and its two HW^2 GEMMs."""
+    def res(px, ci, co):
+        return 2 * 9 * px * (ci * co + co * co) + (2 * px * ci * co if ci != co else 0)
+    px = H * W
+    f = 2 * 9 * px * 4 * 512 + 2 * res(px, 512, 512)
+    f += 4 * 2 * px * 512 * 512 + 2 * 2 * px * px * 512
+    for ci, co, up in ((512, 512, True), (512, 512, True), (512, 256, True), (256, 128, False)):
+        f += res(px, ci, co) + 2 * res(px, co, co)
+        if up:
+            px *= 4
+            f += 2 * 9 * px * co * co
+    return f + 2 * 9 * px * 128 * 3
+
+
 def time_image_path(eng, sdu, rng, reps):
     """The networks around the UNet (seeded weights): CLIP text encoder on a prompt /
-    empty-prompt pair, the TAESD decoder on one 64x64 latent (-> 512x512 image), and the
-    whole sdu_generate call (CLIP, 4-step LCM + CFG at guidance 8, TAESD, host image out).
-    Device-resident inputs except for sdu_generate, whose token ids and image cross PCIe."""
+    empty-prompt pair, the TAESD decoder and the full VAE decoder on one 64x64 latent
+    (-> 512x512 image), and the whole sdu_generate call (CLIP, 4-step LCM + CFG at guidance
+    8, then TAESD, or the full VAE once initialised; host image out).  Device-resident inputs
+    except for sdu_generate, whose token ids and image cross PCIe."""
     import numpy as np
     eng.clip_init(seed=5)
     eng.taesd_init(seed=6)
@@ -126,6 +143,10 @@ def time_image_path(eng, sdu, rng, reps):
     clip_ms = timed(lambda: eng.clip_encode_device(d_ids.ptr, 2, d_ctx.ptr))
     taesd_ms = timed(lambda: eng.taesd_decode_device(d_lat.ptr, 1, 64, 64, d_img.ptr))
     gen_ms = timed(lambda: eng.generate(ids[0], ids[1], 64, 64, 4, 8.0, 4, 42))
+    eng.vae_init(seed=7)
+    vae_ms = timed(lambda: eng.vae_decode_device(d_lat.ptr, 1, 64, 64, d_img.ptr))
+    gen_vae_ms = timed(lambda: eng.generate(ids[0], ids[1], 64, 64, 4, 8.0, 4, 42))
+    vae_flop = vae_decode_flop(64, 64)
     # algorithmic work.  CLIP: 2 x 77 tokens, per layer QKV + out-proj (4 C^2) and the MLP
     # (2 C 3072) per token, plus causal attention counted dense (4 B heads S^2 d).
     T = 2 * 77
@@ -139,6 +160,9 @@ def time_image_path(eng, sdu, rng, reps):
             "taesd_tflops": round(taesd_flop / taesd_ms / 1e9, 1),
             "taesd_frac_mfma": round(taesd_flop / taesd_ms / 1e9 / PEAK_MFMA_TFLOPS, 4),
             "generate_512px_ms": round(gen_ms, 3), "generate_images_per_s": round(1e3 / gen_ms, 2),
+            "vae_decode_64x64_ms": round(vae_ms, 3), "vae_tflops": round(vae_flop / vae_ms / 1e9, 1),
+            "vae_frac_mfma": round(vae_flop / vae_ms / 1e9 / PEAK_MFMA_TFLOPS, 4),
+            "generate_vae_512px_ms": round(gen_vae_ms, 3),
             "reps": reps, "weights": "seeded random (CLIP N(0,0.02), TAESD convs N(0,0.04))"}
 
 

@@ -138,6 +138,19 @@ int sdu_taesd_init(sdu_ctx* ctx, const char* weights_dir, uint64_t seed, int fla
 int sdu_taesd_decode(sdu_ctx* ctx, const float* lat, int B, int H, int W, float* img);
 int sdu_taesd_decode_device(sdu_ctx* ctx, const float* d_lat, int B, int H, int W, float* d_img);
 
+/* Full VAE decoder: replaces vaeDecode with gpu_vae.tflite (VulkanUnetPipeline.kt:55-61;
+ * contract GpuMonoPipeline.kt:26, latents [1,4,64,64] -> image [1,3,512,512] in [-1, 1]), the
+ * LiteRT export of the SD1.5 AutoencoderKL decoder applied as vae.decode(z / 0.18215)
+ * (tools/export_taesd.py:53).  sdu_vae_init creates the decoder's weights: from weights_dir
+ * (one raw fp16 file per diffusers key, post_quant_conv.* and decoder.*, Linear [in, out])
+ * or, when weights_dir is NULL, seeded (conv weights N(0, 0.02), the attention's Linear
+ * weights N(0, 0.1); norms gamma 1 / beta 0 and biases 0, or the affine mode).  Decode: fp32
+ * UNet latent [B,4,H,W] -> fp32 image [B,3,8H,8W] (B 1..4, H and W >= 8, H * W <= 96 * 96),
+ * one captured graph per shape. */
+int sdu_vae_init(sdu_ctx* ctx, const char* weights_dir, uint64_t seed, int flags);
+int sdu_vae_decode(sdu_ctx* ctx, const float* lat, int B, int H, int W, float* img);
+int sdu_vae_decode_device(sdu_ctx* ctx, const float* d_lat, int B, int H, int W, float* d_img);
+
 /* Text encoder: replaces clipContext (VulkanUnetPipeline.kt:48-53), the LiteRT export of SD1.5's
  * CLIP text encoder (CLIPTextModel): int32 token ids [B,77] -> fp32 last hidden state
  * [B,77,768], the UNet's context (B 1..64).  Weights from weights_dir (text_model.* keys,
@@ -150,8 +163,9 @@ int sdu_clip_encode_device(sdu_ctx* ctx, const int32_t* d_ids, int B, float* d_o
 /* End-to-end image: VulkanUnetPipeline.generate (VulkanUnetPipeline.kt:63-97).  CLIP of the
  * prompt and empty-prompt ids in one batch, an initial latent N(0, 1) drawn on the device from
  * `seed`, the LCM denoise of sdu_denoise_lcm_ex (steps, guidance, cfg_steps, noise from
- * `seed`), then the TAESD decoder.  image: fp32 [3, 8H, 8W] in about [-1, 1] (toBitmap,
- * :99-109, maps (x + 1) * 127.5).  Needs sdu_clip_init and sdu_taesd_init. */
+ * `seed`), then the full VAE decoder (sdu_vae_init) when it was initialised, else the TAESD
+ * decoder.  image: fp32 [3, 8H, 8W] in about [-1, 1] (toBitmap, :99-109, maps (x + 1) *
+ * 127.5).  Needs sdu_clip_init and sdu_vae_init or sdu_taesd_init. */
 int sdu_generate(sdu_ctx* ctx, const int32_t* cond_ids, const int32_t* uncond_ids, int H, int W,
                  int steps, float guidance, int cfg_steps, uint64_t seed, float* image);
 

@@ -211,6 +211,7 @@ int sdu_release(sdu_ctx* ctx) {
     free_fwd_states(c);
     aux_free(c.taesd);
     aux_free(c.clip);
+    aux_free(c.vae);
     if (c.wpool) hipFree(c.wpool);
     if (c.op_ws) hipFree(c.op_ws);
     hipStreamDestroy(c.stream);
@@ -371,6 +372,40 @@ int sdu_taesd_decode(sdu_ctx* ctx, const float* lat, int B, int H, int W, float*
     });
 }
 
+int sdu_vae_init(sdu_ctx* ctx, const char* weights_dir, uint64_t seed, int flags) {
+    SDU_GUARD(ctx);
+    if (flags & ~SDU_INIT_RANDOM_AFFINE) return fail(ctx, SDU_ERR_ARG, "bad flags");
+    return guarded(ctx, [&] { return vae_create(ctx->c, weights_dir, seed, flags); });
+}
+
+int sdu_vae_decode_device(sdu_ctx* ctx, const float* d_lat, int B, int H, int W, float* d_img) {
+    SDU_GUARD(ctx);
+    if (!d_lat || !d_img) return fail(ctx, SDU_ERR_ARG, "null argument");
+    return guarded(ctx, [&] { return vae_decode_device(ctx->c, d_lat, B, H, W, d_img); });
+}
+
+int sdu_vae_decode(sdu_ctx* ctx, const float* lat, int B, int H, int W, float* img) {
+    SDU_GUARD(ctx);
+    if (!lat || !img) return fail(ctx, SDU_ERR_ARG, "null argument");
+    if (B < 1 || B > 4 || H < 8 || W < 8 || H * W > 96 * 96)
+        return fail(ctx, SDU_ERR_ARG, "VAE decode: B in 1..4, H and W >= 8, H * W <= 96 * 96");
+    return guarded(ctx, [&]() -> int {
+        const size_t ni = (size_t)B * 4 * H * W, no = (size_t)B * 3 * 64 * H * W;
+        float* d = nullptr;
+        hipError_t e = hipMalloc(&d, (ni + no) * 4);
+        if (e != hipSuccess) return fail(ctx, SDU_ERR_OOM, "staging allocation failed");
+        hipStream_t s = ctx->c.stream;
+        int st = SDU_OK;
+        if ((e = hipMemcpyAsync(d, lat, ni * 4, hipMemcpyHostToDevice, s))) st = hipfail(ctx, e, "upload");
+        if (!st) st = vae_decode_device(ctx->c, d, B, H, W, d + ni);
+        if (!st && ((e = hipMemcpyAsync(img, d + ni, no * 4, hipMemcpyDeviceToHost, s)) || (e = hipStreamSynchronize(s))))
+            st = hipfail(ctx, e, "download");
+        hipStreamSynchronize(s);
+        hipFree(d);
+        return st;
+    });
+}
+
 int sdu_clip_init(sdu_ctx* ctx, const char* weights_dir, uint64_t seed, int flags) {
     SDU_GUARD(ctx);
     if (flags & ~SDU_INIT_RANDOM_AFFINE) return fail(ctx, SDU_ERR_ARG, "bad flags");
@@ -409,7 +444,8 @@ int sdu_generate(sdu_ctx* ctx, const int32_t* cond_ids, const int32_t* uncond_id
                  float guidance, int cfg_steps, uint64_t seed, float* image) {
     SDU_GUARD(ctx);
     if (!cond_ids || !uncond_ids || !image) return fail(ctx, SDU_ERR_ARG, "null argument");
-    if (!ctx->c.clip || !ctx->c.taesd) return fail(ctx, SDU_ERR_WEIGHT, "sdu_generate needs sdu_clip_init and sdu_taesd_init");
+    if (!ctx->c.clip || !(ctx->c.vae || ctx->c.taesd))
+        return fail(ctx, SDU_ERR_WEIGHT, "sdu_generate needs sdu_clip_init and sdu_vae_init or sdu_taesd_init");
     if (H < 8 || W < 8 || H > 128 || W > 128 || H % 8 || W % 8) return fail(ctx, SDU_ERR_ARG, "H, W: multiples of 8 in 8..128");
     return guarded(ctx, [&]() -> int {
         const size_t L = 77, C = 768, nl = (size_t)4 * H * W, ni = (size_t)3 * 64 * H * W;
@@ -434,7 +470,8 @@ int sdu_generate(sdu_ctx* ctx, const int32_t* cond_ids, const int32_t* uncond_id
         if (!st) st = clip_encode_device(c, d_ids, 2, d_ctx);
         if (!st) st = unet_denoise_device(c, d_lat, d_ctx, d_ctx + L * C, H, W, (int)L, steps, guidance, cfg_steps,
                                           nullptr, seed, d_x);
-        if (!st) st = taesd_decode_device(c, d_x, 1, H, W, d_img);
+        // the full VAE (VulkanUnetPipeline.kt:55-61) when initialised, else TAESD
+        if (!st) st = c.vae ? vae_decode_device(c, d_x, 1, H, W, d_img) : taesd_decode_device(c, d_x, 1, H, W, d_img);
         if (!st && ((e = hipMemcpyAsync(image, d_img, ni * 4, hipMemcpyDeviceToHost, s)) || (e = hipStreamSynchronize(s))))
             st = hipfail(ctx, e, "download");
         hipStreamSynchronize(s);

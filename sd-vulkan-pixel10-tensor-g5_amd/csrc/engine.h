@@ -95,7 +95,7 @@ struct AuxState;  // per-shape graph state of an auxiliary network (taesd.cpp, c
 // the CLIP text encoder.  Its own fp16 pool, in the device layouts its kernels read,
 // registered and loaded like the UNet's (same seeded generator, same weight-file format).
 struct AuxNet {
-    int kind = 0;  // AUX_TAESD | AUX_CLIP
+    int kind = 0;  // AUX_TAESD | AUX_CLIP | AUX_VAE
     f16* pool = nullptr;
     size_t pool_bytes = 0;
     std::vector<WeightRec> weights;
@@ -106,6 +106,11 @@ struct AuxNet {
     // TAESD: conv_out with the output affine y = 2 x - 1 folded in (2 W fp16, 2 b - 1 fp32)
     f16* w_out2 = nullptr;
     float* b_out2 = nullptr;
+    // VAE: [conv2 | shortcut] weights and biases of the two width-changing resnets, and the
+    // attention's fp32 to_out bias with to_v's folded in
+    f16* w2sc[2] = {nullptr, nullptr};
+    f16* b2sc[2] = {nullptr, nullptr};
+    float* b_attn_out = nullptr;
     int add(const std::string& name, std::vector<int64_t> shape, int kind, int layout = GL_PLAIN, int ci_pad = 0,
             bool follows = false);
     const WeightRec* w(const std::string& name) const {
@@ -117,7 +122,7 @@ struct AuxNet {
         return r ? r->dev : nullptr;
     }
 };
-enum AuxKind { AUX_TAESD = 1, AUX_CLIP = 2 };
+enum AuxKind { AUX_TAESD = 1, AUX_CLIP = 2, AUX_VAE = 3 };
 
 struct Ctx {
     int device = 0;
@@ -150,6 +155,7 @@ struct Ctx {
     // auxiliary networks (created on demand by sdu_taesd_init / sdu_clip_init)
     AuxNet* taesd = nullptr;
     AuxNet* clip = nullptr;
+    AuxNet* vae = nullptr;
 
     // profiling
     bool profiling = false;
@@ -194,6 +200,9 @@ int set_err(Ctx* c, int code, const std::string& msg);
 // taesd.cpp: latent [B, 4, H, W] fp32 -> image [B, 3, 8H, 8W] fp32 in about [-1, 1]
 int taesd_create(Ctx& c, const char* weights_dir, uint64_t seed, int flags);
 int taesd_decode_device(Ctx& c, const float* d_lat, int B, int H, int W, float* d_img);
+// vae.cpp: UNet latent [B, 4, H, W] fp32 -> image [B, 3, 8H, 8W] fp32 in about [-1, 1]
+int vae_create(Ctx& c, const char* weights_dir, uint64_t seed, int flags);
+int vae_decode_device(Ctx& c, const float* d_lat, int B, int H, int W, float* d_img);
 // clip.cpp: token ids [B, 77] -> last hidden state [B, 77, 768] fp32
 int clip_create(Ctx& c, const char* weights_dir, uint64_t seed, int flags);
 int clip_encode_device(Ctx& c, const int32_t* d_ids, int B, float* d_out);

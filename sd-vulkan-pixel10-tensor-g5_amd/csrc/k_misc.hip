@@ -38,6 +38,82 @@ hipError_t nchw_to_nhwc_launch(const float* src, f16* dst, int B, int Bsrc, int 
     return hipGetLastError();
 }
 
+// The VAE decoder's input: the UNet latent z (NCHW fp32 [B,4,H,W]) divided by the
+// scaling factor and through post_quant_conv (1x1, 4 -> 4, fp32 arithmetic), as NHWC
+// fp16 [B,H,W,8] with channels 4..7 zero.  One thread per pixel, one 16-byte store.
+__global__ void vae_stage_kernel(const float* z, const f16* w, const f16* bias, f16* y, int B, int HW,
+                                 float inv_scale) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)B * HW) return;
+    const int b = (int)(i / HW), p = (int)(i % HW);
+    float zi[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) zi[c] = z[((int64_t)b * 4 + c) * HW + p] * inv_scale;
+    uint4 o = make_uint4(0, 0, 0, 0);
+    f16* oh = (f16*)&o;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        float acc = (float)bias[c];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) acc += (float)w[c * 4 + k] * zi[k];
+        oh[c] = (f16)acc;
+    }
+    *(uint4*)(y + i * 8) = o;
+}
+
+hipError_t vae_stage_launch(const float* z, const f16* w, const f16* bias, f16* y, int B, int HW, float inv_scale,
+                            hipStream_t s) {
+    if (B < 1 || HW < 1) return hipErrorInvalidValue;
+    const int64_t n = (int64_t)B * HW;
+    launch_timed("vae_stage_kernel", 32.0 * n, 16.0 * n + 16.0 * n, [&] {
+        SDU_LAUNCH(vae_stage_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, z, w, bias, y, B, HW,
+                   inv_scale);
+    });
+    return hipGetLastError();
+}
+
+// Softmax of the rows of an fp32 score matrix [rows][n] (row stride n) times `scale`,
+// stored fp16 [rows][n]: one 256-thread block per row; max, then the sum of
+// 2^((s - max) * scale * log2 e), then the normalised values.
+__device__ __forceinline__ float block_reduce(float v, bool is_max, float* red) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float o = __shfl_xor(v, off);
+        v = is_max ? fmaxf(v, o) : v + o;
+    }
+    const int w = threadIdx.x >> 6;
+    __syncthreads();  // red reused across calls
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    v = red[0];
+#pragma unroll
+    for (int i = 1; i < 4; ++i) v = is_max ? fmaxf(v, red[i]) : v + red[i];
+    return v;
+}
+
+__global__ __launch_bounds__(256) void softmax_rows_kernel(const float* s, f16* p, int n, float c) {
+    __shared__ float red[4];
+    const float* sr = s + (int64_t)blockIdx.x * n;
+    f16* pr = p + (int64_t)blockIdx.x * n;
+    float m = -INFINITY;
+    for (int j = threadIdx.x; j < n; j += 256) m = fmaxf(m, sr[j]);
+    m = block_reduce(m, true, red);
+    float sum = 0.f;
+    for (int j = threadIdx.x; j < n; j += 256) sum += __builtin_amdgcn_exp2f((sr[j] - m) * c);
+    sum = block_reduce(sum, false, red);
+    const float inv = 1.0f / sum;
+    for (int j = threadIdx.x; j < n; j += 256) pr[j] = (f16)(__builtin_amdgcn_exp2f((sr[j] - m) * c) * inv);
+}
+
+hipError_t softmax_rows_launch(const float* s, f16* p, int rows, int n, float scale, hipStream_t st) {
+    if (rows < 1 || n < 1) return hipErrorInvalidValue;
+    const float c = scale * 1.4426950408889634f;
+    launch_timed("softmax_rows_kernel", 0.0, (double)rows * n * 6.0, [&] {
+        SDU_LAUNCH(softmax_rows_kernel, dim3((unsigned)rows), dim3(256), 0, st, s, p, n, c);
+    });
+    return hipGetLastError();
+}
+
 // The UNet forward's inputs in one launch, outside its graph: the latent NCHW fp32
 // [B,C,H,W] -> NHWC fp16 [B,H,W,Cpad] (channels >= C zero), the context fp32 -> fp16,
 // and ntemb floats of the time projection copied.  Threads [0, nlat) take the latent,

@@ -193,6 +193,12 @@ hipError_t layernorm_launch(const f16* x, const f16* gamma, const f16* beta, f16
 // TAESD decoder's input clamp).
 hipError_t nchw_to_nhwc_launch(const float* src, f16* dst, int B, int Bsrc, int C, int Cpad, int HW,
                                hipStream_t s, int tanh_clamp = 0);
+// The VAE decoder's input stage: NHWC fp16 [B,H,W,8] = post_quant_conv(z * inv_scale)
+// (w [4][4], bias [4]) from the NCHW fp32 latent [B,4,H,W]; channels 4..7 zero.
+hipError_t vae_stage_launch(const float* z, const f16* w, const f16* bias, f16* y, int B, int HW, float inv_scale,
+                            hipStream_t s);
+// p[r][j] = fp16(softmax_j(scale * s[r][:])) for an fp32 [rows][n] score matrix.
+hipError_t softmax_rows_launch(const float* s, f16* p, int rows, int n, float scale, hipStream_t st);
 // The UNet forward's inputs in one launch: latent NCHW fp32 [B,C,H,W] -> NHWC fp16
 // [B,H,W,Cpad], context fp32 -> fp16 (nctx values), ntemb time-projection floats copied
 // to temb_dst (ntemb 0: none).  The same launch clears zero_bytes (rounded up to 16) at

@@ -25,41 +25,9 @@ thread_local KernelTimer* g_kernel_timer = nullptr;
 thread_local hipEvent_t g_launch_ev0 = nullptr, g_launch_ev1 = nullptr;
 
 
-// An activation with, when its producing GEMM kept them, the per-channel sums and sums
-// of squares [B][C][2] of its values (for the GroupNorm that reads it).
-struct Act {
-    const f16* p;
-    const double* st;
-};
-
-// Statistics slot for a GEMM output of N channels over images of HW pixels, or null
-// (then the GroupNorm that reads the output computes its own statistics).
-static void want_stats(Exec& E, GemmArgs& a, int HW) {
-    const size_t n = (size_t)E.B * a.N * 2;
-    // up to 32x32 pixels the GroupNorm's own single-kernel statistics pass (one block
-    // per group and image) costs less than the epilogue statistics and their apply
-    if (HW <= 1024 || !gemm_stats_supported(HW) || E.st_next == nullptr || E.st_next + n > E.st_end) return;
-    a.stats = E.st_next;
-    a.stats_hw = HW;
-    E.st_next += n;
-}
-
 static void groupnorm(Exec& E, Act x, Act x2, int C1, int C2, const f16* g, const f16* b, f16* y, int HW,
                       int silu) {
-    char shape[48];
-    snprintf(shape, sizeof shape, "HW=%d C=%d", HW, C1 + C2);
-    if (x.st && (C2 == 0 || x2.st)) {
-        E.run(silu ? "groupnorm_silu" : "groupnorm", [&] {
-            return groupnorm_apply_stats_launch(x.p, x2.p, C1, C2, x.st, x2.st, g, b, y, E.B, HW, kGroups, kEps,
-                                                silu, E.s);
-        }, shape);
-        return;
-    }
-    double* acc = E.gn_acc;
-    E.gn_acc += (size_t)E.B * kGroups * 2;
-    E.run(silu ? "groupnorm_silu" : "groupnorm", [&] {
-        return groupnorm_launch(x.p, x2.p, C1, C2, g, b, y, E.B, HW, kGroups, kEps, silu, acc, E.s);
-    }, shape);
+    group_norm_op(E, x, x2, C1, C2, g, b, y, HW, silu, kEps);
 }
 
 static void attention(Exec& E, const char* cat, const f16* q, const f16* k, const f16* v, f16* o,

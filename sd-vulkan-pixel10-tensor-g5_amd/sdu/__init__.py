@@ -44,7 +44,8 @@ EXPORTS = [
     "sdu_tensor_alloc", "sdu_tensor_free", "sdu_tensor_upload", "sdu_tensor_download",
     "sdu_tensor_device_ptr", "sdu_tensor_bytes", "sdu_groupnorm", "sdu_groupnorm_noalloc", "sdu_layernorm", "sdu_matmul",
     "sdu_conv2d", "sdu_conv2d_groupnorm", "sdu_attention", "sdu_attention_ex", "sdu_geglu", "sdu_silu", "sdu_add", "sdu_add_bias",
-    "sdu_lcm_step", "sdu_taesd_init", "sdu_taesd_decode", "sdu_taesd_decode_device", "sdu_clip_init",
+    "sdu_lcm_step", "sdu_taesd_init", "sdu_taesd_decode", "sdu_taesd_decode_device", "sdu_vae_init",
+    "sdu_vae_decode", "sdu_vae_decode_device", "sdu_clip_init",
     "sdu_clip_encode", "sdu_clip_encode_device", "sdu_generate", "sdu_calibrate",
 ]
 
@@ -124,6 +125,9 @@ def load(path: str = LIB_PATH):
         "sdu_taesd_init": ([P, ctypes.c_char_p, ctypes.c_uint64, I], I),
         "sdu_taesd_decode": ([P, P, I, I, I, P], I),
         "sdu_taesd_decode_device": ([P, P, I, I, I, P], I),
+        "sdu_vae_init": ([P, ctypes.c_char_p, ctypes.c_uint64, I], I),
+        "sdu_vae_decode": ([P, P, I, I, I, P], I),
+        "sdu_vae_decode_device": ([P, P, I, I, I, P], I),
         "sdu_clip_init": ([P, ctypes.c_char_p, ctypes.c_uint64, I], I),
         "sdu_clip_encode": ([P, P, I, P], I),
         "sdu_clip_encode_device": ([P, P, I, P], I),
@@ -393,6 +397,19 @@ class Engine:
 
     def taesd_decode_device(self, d_lat: int, B, H, W, d_img: int):
         self._check(load().sdu_taesd_decode_device(self.h, d_lat, B, H, W, d_img))
+
+    def vae_init(self, weights_dir: Optional[str] = None, seed: int = 0, flags: int = 0):
+        self._check(load().sdu_vae_init(self.h, weights_dir.encode() if weights_dir else None, seed, flags))
+
+    def vae_decode(self, lat: np.ndarray) -> np.ndarray:
+        lat = np.ascontiguousarray(lat, np.float32)
+        B, _, H, W = lat.shape
+        out = np.empty((B, 3, 8 * H, 8 * W), np.float32)
+        self._check(load().sdu_vae_decode(self.h, _ptr(lat), B, H, W, _ptr(out)))
+        return out
+
+    def vae_decode_device(self, d_lat: int, B, H, W, d_img: int):
+        self._check(load().sdu_vae_decode_device(self.h, d_lat, B, H, W, d_img))
 
     def clip_init(self, weights_dir: Optional[str] = None, seed: int = 0, flags: int = 0):
         self._check(load().sdu_clip_init(self.h, weights_dir.encode() if weights_dir else None, seed, flags))
