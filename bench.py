@@ -163,7 +163,7 @@ def time_image_path(eng, sdu, rng, reps):
             "vae_decode_64x64_ms": round(vae_ms, 3), "vae_tflops": round(vae_flop / vae_ms / 1e9, 1),
             "vae_frac_mfma": round(vae_flop / vae_ms / 1e9 / PEAK_MFMA_TFLOPS, 4),
             "generate_vae_512px_ms": round(gen_vae_ms, 3),
-            "reps": reps, "weights": "seeded random (CLIP N(0,0.02), TAESD convs N(0,0.04))"}
+            "reps": reps, "weights": "seeded random (CLIP N(0,0.02), TAESD convs N(0,0.04), VAE convs N(0,0.02) and attention Linear N(0,0.1))"}
 
 
 # The reference's own micro-benchmark shapes (VulkanBench.kt:72-118), timed per op with
