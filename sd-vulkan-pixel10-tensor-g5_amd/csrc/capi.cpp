@@ -975,7 +975,15 @@ int sdu_attention_ex(sdu_ctx* ctx, const sdu_tensor* q, const sdu_tensor* k, con
         !fits(v, (size_t)B * Sk * ldv * 2) || !fits(o, (size_t)B * Sq * ldo * 2))
         return fail(ctx, SDU_ERR_ARG, "attention tensor too small");
     AttnArgs a{(const f16*)dptr(q), (const f16*)dptr(k), (const f16*)dptr(v), (f16*)dptr(o), B, heads, Sq, Sk,
-               d, ldq, ldk, ldv, ldo, scale, causal, (flags & SDU_ATTN_Q_LOG2) != 0};
+               d, ldq, ldk, ldv, ldo, scale, causal, (flags & SDU_ATTN_Q_LOG2) != 0, nullptr, 0};
+    const size_t ws = attention_workspace_bytes(a);
+    if (ws) {
+        const int st = ensure_op_ws(ctx->c, ws);
+        if (st) return st;
+        const hipError_t e = zero_launch(ctx->c.op_ws, gemm_counter_bytes(), ctx->c.stream);
+        if (e != hipSuccess) return finish(ctx, e, "attention");
+        a.ws = ctx->c.op_ws;
+    }
     return finish(ctx, attention_launch(a, ctx->c.stream), "attention");
 }
 

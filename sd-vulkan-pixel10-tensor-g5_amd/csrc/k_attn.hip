@@ -40,6 +40,10 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 static constexpr float kRescaleLog2 = 8.0f;  // lazy-rescale threshold (log2 units)
+// key-split shared-tile launches: pair counters at the head of the workspace (one per
+// query block, head and image; zero between launches), the partial slots after them
+static constexpr int kAttnMaxPairs = 16384;
+static constexpr int kAttnCounterFloats = kAttnMaxPairs;
 
 __device__ __forceinline__ int key_perm(int r) {
     const int o = r & 15;
@@ -182,7 +186,10 @@ __device__ __forceinline__ void vt_pad_rows(f16* vt, int vstr, int keys, int d, 
 // per CU: half the barriers and per-tile softmax overhead per key).
 // OFS: Q holds q * scale * log2 e and head dimension d (< KS*16) carries the softmax
 // reference (ofs_update): K's column d is 1 and Q's dimension d is -m_run.
-template <int KS, int MTD, int NWAVE, bool LSUM, int KT = 64, bool OFS = false>
+// SPL: the keys are split in two parts at a.kpart (a multiple of KT), blockIdx.z = image * 2 +
+// part; each part's block stores its unnormalised O^T, reference and row-sum partial into a
+// workspace slot, and the pair's second block to finish merges both (see the end).
+template <int KS, int MTD, int NWAVE, bool LSUM, int KT = 64, bool OFS = false, bool SPL = false>
 __global__ __launch_bounds__(NWAVE * 64) void attn_kernel(AttnArgs a) {
     constexpr int VSTR = KT + 8;  // Vt row stride (halves)
     constexpr int NSUB = KT / 32;
@@ -192,7 +199,9 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_kernel(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) f16 Vt[2][MTD * 32 * VSTR];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int h = blockIdx.y, b = blockIdx.z;
+    const int h = blockIdx.y;
+    const int b = SPL ? (int)(blockIdx.z >> 1) : (int)blockIdx.z, part = SPL ? (int)(blockIdx.z & 1) : 0;
+    const int kbeg = part * a.kpart, nkeys = (SPL && part == 0 ? a.kpart : a.Sk) - kbeg;  // this block's keys
     const int d = a.d, dch = d >> 3;  // 16-byte chunks per row
     const int q0 = blockIdx.x * (NWAVE * 32) + wave * 32;
     const int lrow = lane & 31, hl = lane >> 5, lk = hl * 8;
@@ -230,12 +239,12 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_kernel(AttnArgs a) {
     // 0) and move by one add per tile; keys past Sk and threads without a chunk read
     // past the resource's range and get zeros.  No branches, so all loads of a tile
     // stay in flight while the current tile is computed.
-    const f16* kbase = a.k + (int64_t)b * a.Sk * a.ldk + (int64_t)h * d;
-    const f16* vbase = a.v + (int64_t)b * a.Sk * a.ldv + (int64_t)h * d;
+    const f16* kbase = a.k + ((int64_t)b * a.Sk + kbeg) * a.ldk + (int64_t)h * d;
+    const f16* vbase = a.v + ((int64_t)b * a.Sk + kbeg) * a.ldv + (int64_t)h * d;
     const __amdgpu_buffer_rsrc_t rsk = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)kbase, (short)0, ((a.Sk - 1) * a.ldk + d) * 2, 0x00020000);
+        (void*)kbase, (short)0, ((nkeys - 1) * a.ldk + d) * 2, 0x00020000);
     const __amdgpu_buffer_rsrc_t rsv = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)vbase, (short)0, ((a.Sk - 1) * a.ldv + d) * 2, 0x00020000);
+        (void*)vbase, (short)0, ((nkeys - 1) * a.ldv + d) * 2, 0x00020000);
     // K: one 16-byte chunk (8 dims of one key) per thread and step, stored as is.
     // V: one unit = the same 8 dims of 4 consecutive keys per thread and step, so that
     // the transposed store to V^T [dim][key] is 8 ds_write_b64 (4 keys of one dim each)
@@ -302,7 +311,7 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_kernel(AttnArgs a) {
         }
     };
 
-    const int nt = (a.Sk + KT - 1) / KT;
+    const int nt = (nkeys + KT - 1) / KT;
     load_kv(0);
     __syncthreads();  // padding set before the first tile stores land next to it
     store_kv(0);
@@ -331,7 +340,7 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_kernel(AttnArgs a) {
             }
         };
         qk();
-        const int kvalid = min(KT, a.Sk - kb);
+        const int kvalid = min(KT, nkeys - kb);
         if constexpr (OFS) {
             if (ofs_update<NSUB, MTD>(s, kvalid, m_run, l_run, o, hl, it == 0)) {
                 // Q's dimension d (k-step d / 16, lanes of half (d / 8) & 1, element 0)
@@ -356,8 +365,72 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_kernel(AttnArgs a) {
         __syncthreads();
     }
 
-    const float inv = 1.0f / row_sum<MTD, LSUM>(o, l_run, lrow);
+    const float lsum = row_sum<MTD, LSUM>(o, l_run, lrow);
+    const float inv = 1.0f / lsum;
     const int q = q0 + lrow;
+    if constexpr (SPL) {
+        // This part's normalised output O_p (fp32, the head's d dims), its reference m_p
+        // and row sum l_p go to the pair's workspace slot; the pair's second block to
+        // finish writes (W_0 O_0 + W_1 O_1) / (W_0 + W_1), W_p = l_p 2^(m_p - max m), reading
+        // both parts in part order (its own re-read), so the result does not depend on
+        // which finished last.  Ordering as in the GEMM's in-kernel split-K sum:
+        // device-coherent (sc1) buffer stores, each wave's vmcnt(0) before the block
+        // barrier, a device-scope atomic on the pair's counter, the second block's sc1
+        // loads only after the barrier that follows its read of the count.  (Normalised
+        // values stored like the output path keep the accumulators in one register
+        // range through the key loop.)
+        constexpr int CPOL_SC1 = 1 << 4;
+        constexpr int PW = (MTD * 16 + 2) * 64;  // floats per wave and part: [MTD*16 + 2][64 lanes]
+        __shared__ int last_flag;
+        const int blk = (b * a.heads + h) * gridDim.x + blockIdx.x;
+        const __amdgpu_buffer_rsrc_t rsP = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(a.ws + kAttnCounterFloats + (int64_t)blk * 2 * NWAVE * PW), (short)0, 2 * NWAVE * PW * 4, 0x00020000);
+        const uint32_t vo = (uint32_t)((wave * PW + lane) * 4);
+        const int pso = NWAVE * PW * 4;  // bytes per part
+#pragma unroll
+        for (int t = 0; t < MTD; ++t)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int dim = t * 32 + (e >> 2) * 8 + hl * 4 + (e & 3);
+                if (dim < d)
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, o[t][e] * inv), rsP,
+                                                          vo + (t * 16 + e) * 256, part * pso, CPOL_SC1);
+            }
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, m_run), rsP, vo + MTD * 16 * 256,
+                                              part * pso, CPOL_SC1);
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, lsum), rsP, vo + (MTD * 16 + 1) * 256,
+                                              part * pso, CPOL_SC1);
+        __builtin_amdgcn_s_waitcnt((0 & 0xF) | (0x7 << 4) | (0x0 << 8));  // vmcnt(0): this wave's stores are done
+        __syncthreads();
+        if (tid == 0) {
+            unsigned* cnt = (unsigned*)a.ws + blk;
+            const unsigned prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const bool last = prev == 1u;
+            if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // for the next launch
+            last_flag = last;
+        }
+        __syncthreads();
+        if (!last_flag) return;
+        auto ld = [&](int pp, int j) {
+            return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsP, vo + j * 256, pp * pso, CPOL_SC1));
+        };
+        const float m0 = ld(0, MTD * 16), m1 = ld(1, MTD * 16);
+        const float mm = fmaxf(m0, m1);
+        const float w0 = ld(0, MTD * 16 + 1) * fast_exp2(m0 - mm), w1 = ld(1, MTD * 16 + 1) * fast_exp2(m1 - mm);
+        const float wn = 1.0f / (w0 + w1);
+        if (q < a.Sq) {
+            f16* op = a.o + ((int64_t)b * a.Sq + q) * a.ldo + (int64_t)h * d;
+#pragma unroll
+            for (int t = 0; t < MTD; ++t)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int dim = t * 32 + (e >> 2) * 8 + hl * 4 + (e & 3);
+                    if (dim < d) op[dim] = (f16)((w0 * ld(0, t * 16 + e) + w1 * ld(1, t * 16 + e)) * wn);
+                }
+        }
+        return;
+    }
+
     if (q < a.Sq) {
         f16* op = a.o + ((int64_t)b * a.Sq + q) * a.ldo + (int64_t)h * d;
 #pragma unroll
@@ -549,13 +622,36 @@ __global__ __launch_bounds__(NSPLIT * 64) void attn_split_kernel(AttnArgs a) {
 
 // ----------------------------------------------------------------- launch
 
+// Blocks of one shared-tile variant resident on the whole chip at once (its occupancy
+// per CU times the CUs), queried once per variant (the template arguments name it).
+template <int KS, int MTD, bool LSUM, bool OFS, class Kern>
+static int resident_blocks(Kern kern, int threads) {
+    static int n = -1;
+    if (n < 0) {
+        int dev = 0, cus = 0, per = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kern, threads, 0) != hipSuccess)
+            cus = per = 0;
+        n = cus * per;
+    }
+    return n;
+}
+
+// How a launch runs: the shared-tile kernel (waves per block, 128-key tiles, the softmax
+// reference in a spare dimension, keys split in two) or the key-split kernel (waves per
+// 32-query group).
+struct AttnPlan {
+    bool shared;
+    int nw, ns;
+    bool kt128, ofs, spl;
+    dim3 grid;
+};
+
 template <int KS, int MTD, bool LSUM>
-static void launch_cfg(const AttnArgs& a, hipStream_t s) {
+static AttnPlan attn_plan(const AttnArgs& a) {
+    AttnPlan p{};
     const int64_t bh = (int64_t)a.heads * a.B;
     const int64_t qwaves = ((a.Sq + 31) / 32) * bh;  // one wave per 32 queries
-    const double flops = 4.0 * bh * a.Sq * a.Sk * a.d;
-    const double bytes = 2.0 * bh * a.d * (2.0 * a.Sq + 2.0 * a.Sk);
-    char name[48];
     // shared K/V tiles where there are enough query waves to fill the chip (the
     // key-split kernel re-reads K/V per wave): four query waves per block, eight for
     // heads of 56..128 when four would leave < 512 blocks (their larger K/V tiles are
@@ -565,25 +661,29 @@ static void launch_cfg(const AttnArgs& a, hipStream_t s) {
     // short key sequences (cross-attention over the 77 context tokens), go to the
     // key-split kernel: its extra waves, or not staging a few K/V tiles per block, win.
     if (qwaves >= 1024 && a.Sk > 128 && !a.causal) {
-        const int nw = (a.d > 48 && a.d <= 128 && ((a.Sq + 127) / 128) * bh < 512) ? 8 : 4;
-        const dim3 grid((a.Sq + nw * 32 - 1) / (nw * 32), a.heads, a.B);
+        p.shared = true;
+        p.nw = (a.d > 48 && a.d <= 128 && ((a.Sq + 127) / 128) * bh < 512) ? 8 : 4;
+        p.grid = dim3((a.Sq + p.nw * 32 - 1) / (p.nw * 32), a.heads, a.B);
         // 128-key tiles for heads <= 48 when every block is resident at once (two per CU):
         // d40 at 4096 tokens, B=2, 0.44 ms per forward against 0.46 with 64-key tiles;
         // on larger grids they lose (0.24 ms more at 9216 tokens, 0.31 ms at B=16)
-        const bool kt128 = KS == 3 && nw == 4 && (long)grid.x * bh <= 512;
+        p.kt128 = KS == 3 && p.nw == 4 && (long)p.grid.x * bh <= 512;
         // the softmax reference rides in a spare head dimension when Q is pre-scaled
-        const bool ofs = a.q_log2 && a.d < KS * 16 && nw == 4;
-        snprintf(name, sizeof name, "attn_kernel<%d,%d,%d,%d,%d%s>", KS, MTD, nw, (int)LSUM, kt128 ? 128 : 64,
-                 ofs ? ",1" : "");
-        constexpr int KTB = KS == 3 ? 128 : 64;
-        launch_timed(name, flops, bytes, [&] {
-            if (nw == 8) SDU_LAUNCH((attn_kernel<KS, MTD, 8, LSUM>), grid, dim3(512), 0, s, a);
-            else if (KS == 3 && kt128 && ofs) SDU_LAUNCH((attn_kernel<KS, MTD, 4, LSUM, KTB, true>), grid, dim3(256), 0, s, a);
-            else if (KS == 3 && kt128) SDU_LAUNCH((attn_kernel<KS, MTD, 4, LSUM, KTB>), grid, dim3(256), 0, s, a);
-            else if (ofs) SDU_LAUNCH((attn_kernel<KS, MTD, 4, LSUM, 64, true>), grid, dim3(256), 0, s, a);
-            else SDU_LAUNCH((attn_kernel<KS, MTD, 4, LSUM>), grid, dim3(256), 0, s, a);
-        });
-        return;
+        p.ofs = a.q_log2 && a.d < KS * 16 && p.nw == 4;
+        // Keys split in two when the blocks fill a round and a part of the next: the
+        // half-length blocks then fill whole rounds.  A partial last round is modelled
+        // at 3/4 of a full one's time, the merge at 1/20 (d40 at 9216 tokens, B=2: 1.5
+        // rounds of 768 blocks; measured 1.75 round-times)
+        if (p.nw == 4 && !p.kt128 && a.Sk > 64 && (long)p.grid.x * bh <= kAttnMaxPairs) {
+            const long nblk = (long)p.grid.x * bh;
+            const int slots = p.ofs ? resident_blocks<KS, MTD, LSUM, true>(attn_kernel<KS, MTD, 4, LSUM, 64, true>, 256)
+                                    : resident_blocks<KS, MTD, LSUM, false>(attn_kernel<KS, MTD, 4, LSUM>, 256);
+            if (slots > 0) {
+                auto rounds = [&](double r) { const double f = floor(r); return f + (r > f ? 0.75 : 0.0); };
+                p.spl = rounds(2.0 * nblk / slots) * 0.5 + 0.05 < 0.9 * rounds((double)nblk / slots);
+            }
+        }
+        return p;
     }
     // key split: enough waves to fill the chip, at most one per 32-key tile, and at
     // most 4 for wide heads (LDS for the fp32 merge)
@@ -591,9 +691,51 @@ static void launch_cfg(const AttnArgs& a, hipStream_t s) {
     int ns = (int)((2048 + qwaves - 1) / qwaves);
     if (ns > ntile) ns = ntile;
     const int nmax = MTD > 3 ? 4 : 8;
-    ns = ns <= 1 ? 1 : ns <= 2 ? 2 : (ns <= 4 || nmax == 4) ? 4 : 8;
+    p.ns = ns <= 1 ? 1 : ns <= 2 ? 2 : (ns <= 4 || nmax == 4) ? 4 : 8;
+    p.grid = dim3((a.Sq + 31) / 32, a.heads, a.B);
+    return p;
+}
+
+template <int KS, int MTD, bool LSUM>
+static size_t ws_bytes(const AttnArgs& a) {
+    const AttnPlan p = attn_plan<KS, MTD, LSUM>(a);
+    if (!p.spl) return 0;
+    const size_t pairs = (size_t)p.grid.x * p.grid.y * p.grid.z;
+    return kAttnCounterFloats * 4 + pairs * 2 * 4 * (MTD * 16 + 2) * 64 * 4;  // attn_kernel's SPL slots
+}
+
+template <int KS, int MTD, bool LSUM>
+static void launch_cfg(const AttnArgs& a0, hipStream_t s) {
+    AttnArgs a = a0;
+    const AttnPlan p = attn_plan<KS, MTD, LSUM>(a);
+    const int64_t bh = (int64_t)a.heads * a.B;
+    const double flops = 4.0 * bh * a.Sq * a.Sk * a.d;
+    const double bytes = 2.0 * bh * a.d * (2.0 * a.Sq + 2.0 * a.Sk);
+    char name[48];
+    if (p.shared) {
+        const bool spl = p.spl && a.ws;
+        snprintf(name, sizeof name, "attn_kernel<%d,%d,%d,%d,%d%s%s>", KS, MTD, p.nw, (int)LSUM, p.kt128 ? 128 : 64,
+                 p.ofs || spl ? (p.ofs ? ",1" : ",0") : "", spl ? ",1" : "");
+        constexpr int KTB = KS == 3 ? 128 : 64;
+        dim3 grid = p.grid;
+        if (spl) {
+            a.kpart = ((a.Sk + 127) / 128) * 64;  // half the 64-key tiles (rounded up)
+            grid.z *= 2;
+        }
+        launch_timed(name, flops, bytes, [&] {
+            if (p.nw == 8) SDU_LAUNCH((attn_kernel<KS, MTD, 8, LSUM>), grid, dim3(512), 0, s, a);
+            else if (KS == 3 && p.kt128 && p.ofs) SDU_LAUNCH((attn_kernel<KS, MTD, 4, LSUM, KTB, true>), grid, dim3(256), 0, s, a);
+            else if (KS == 3 && p.kt128) SDU_LAUNCH((attn_kernel<KS, MTD, 4, LSUM, KTB>), grid, dim3(256), 0, s, a);
+            else if (spl && p.ofs) SDU_LAUNCH((attn_kernel<KS, MTD, 4, LSUM, 64, true, true>), grid, dim3(256), 0, s, a);
+            else if (spl) SDU_LAUNCH((attn_kernel<KS, MTD, 4, LSUM, 64, false, true>), grid, dim3(256), 0, s, a);
+            else if (p.ofs) SDU_LAUNCH((attn_kernel<KS, MTD, 4, LSUM, 64, true>), grid, dim3(256), 0, s, a);
+            else SDU_LAUNCH((attn_kernel<KS, MTD, 4, LSUM>), grid, dim3(256), 0, s, a);
+        });
+        return;
+    }
+    const int ns = p.ns;
     snprintf(name, sizeof name, "attn_split_kernel<%d,%d,%d,%d>", KS, MTD, ns, (int)LSUM);
-    const dim3 grid((a.Sq + 31) / 32, a.heads, a.B);
+    const dim3 grid = p.grid;
     launch_timed(name, flops, bytes, [&] {
         if (ns == 1) SDU_LAUNCH((attn_split_kernel<KS, MTD, 1, LSUM>), grid, dim3(64), 0, s, a);
         else if (ns == 2) SDU_LAUNCH((attn_split_kernel<KS, MTD, 2, LSUM>), grid, dim3(128), 0, s, a);
@@ -607,6 +749,23 @@ template <int KS, int MTD>
 static void launch_d(const AttnArgs& a, hipStream_t s) {
     if (a.d < MTD * 32) launch_cfg<KS, MTD, true>(a, s);
     else launch_cfg<KS, MTD, false>(a, s);
+}
+
+template <int KS, int MTD>
+static size_t ws_d(const AttnArgs& a) {
+    return a.d < MTD * 32 ? ws_bytes<KS, MTD, true>(a) : ws_bytes<KS, MTD, false>(a);
+}
+
+size_t attention_workspace_bytes(const AttnArgs& a) {
+    if (a.d <= 0 || a.d > 160 || (a.d & 7) || a.Sq <= 0 || a.Sk <= 0) return 0;
+    const int d = a.d;
+    if (d <= 32) return ws_d<2, 1>(a);
+    if (d <= 48) return ws_d<3, 2>(a);
+    if (d <= 64) return ws_d<4, 2>(a);
+    if (d <= 80) return ws_d<5, 3>(a);
+    if (d <= 96) return ws_d<6, 3>(a);
+    if (d <= 128) return ws_d<8, 4>(a);
+    return ws_d<10, 5>(a);
 }
 
 hipError_t attention_launch(const AttnArgs& a, hipStream_t s) {

@@ -167,8 +167,15 @@ struct AttnArgs {
     float scale;
     int causal;  // query i attends keys 0..i only (Sq == Sk; the CLIP text encoder)
     int q_log2;  // q already holds q * scale * log2 e (the projection folded it in)
+    // Optional workspace (attention_workspace_bytes; its first gemm_counter_bytes() zero on
+    // entry and left zero, as the GEMM's): with it, a shared-tile launch whose blocks would
+    // leave a partly filled last round splits the keys in two and merges the halves.
+    float* ws;
+    int kpart;  // (set by attention_launch)
 };
 hipError_t attention_launch(const AttnArgs& a, hipStream_t s);
+// Workspace bytes attention_launch uses for these arguments when given one (0: none).
+size_t attention_workspace_bytes(const AttnArgs& a);
 
 // ----------------------------------------------------------------- norms
 // GroupNorm accumulator: fp64 [B][G][2] (sum, sum of squares); must be zero on

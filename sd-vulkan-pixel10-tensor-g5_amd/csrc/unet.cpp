@@ -32,9 +32,12 @@ static void groupnorm(Exec& E, Act x, Act x2, int C1, int C2, const f16* g, cons
 
 static void attention(Exec& E, const char* cat, const f16* q, const f16* k, const f16* v, f16* o,
                       int Sq, int Sk, int C, int ldq, int ldk, int ldv) {
-    // q comes from a projection with the softmax factor folded in (attn_qscale)
+    // q comes from a projection with the softmax factor folded in (attn_qscale); the GEMM
+    // workspace serves a key-split launch
     AttnArgs a{q, k, v, o, E.B, kUnetHeads, Sq, Sk, C / kUnetHeads, ldq, ldk, ldv, C,
-               1.0f / sqrtf((float)(C / kUnetHeads)), 0, 1};
+               1.0f / sqrtf((float)(C / kUnetHeads)), 0, 1, E.gemm_ws, 0};
+    const size_t ws = attention_workspace_bytes(a);
+    if (ws > E.gemm_ws_need) E.gemm_ws_need = ws;
     char shape[64];
     snprintf(shape, sizeof shape, "Sq=%d Sk=%d d=%d", Sq, Sk, C / kUnetHeads);
     E.run(cat, [&] { return attention_launch(a, E.s); }, shape);

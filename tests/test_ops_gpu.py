@@ -398,6 +398,10 @@ def test_conv2d_inplace_residual_and_overlap_errors(op_engine):
     # 4 queries) and key count (last 64-key tile with 13)
     (8, 8, 4100, 333, 40),
     (4, 16, 2048, 200, 40),
+    # keys split in two halves merged in-kernel (1.33 and 1.5 rounds of blocks; half a
+    # round, with a ragged key count: halves of 1024 and 976 keys)
+    (2, 8, 9216, 9216, 40),   # UNet 96x96 self-attention
+    (3, 8, 2000, 1000, 40),
 ])
 def test_attention(op_engine, B, heads, Sq, Sk, d):
     say(f"attention B={B} heads={heads} Sq={Sq} Sk={Sk} d={d}")
@@ -448,6 +452,10 @@ def test_attention_strided_rows(op_engine):
     (1, 2, 100, 37, 40),      # key-split kernel (no reference dimension)
     (4, 8, 1000, 700, 80),    # eight-wave shared tiles (d a multiple of 16)
     (2, 8, 256, 256, 160),
+    # keys split in two halves merged in-kernel, with the reference dimension
+    (2, 8, 9216, 9216, 40),   # UNet 96x96 self-attention
+    (3, 8, 2000, 1000, 40),
+    (4, 16, 2048, 200, 40),
 ])
 def test_attention_q_log2(op_engine, B, heads, Sq, Sk, d):
     import sdu
@@ -465,6 +473,9 @@ def test_attention_q_log2(op_engine, B, heads, Sq, Sk, d):
     ref = U.attention(t(qp), t(k), t(v), heads).numpy()
     assert rel_err_l1(got, ref) < 2e-3
     assert np.abs(got - ref).max() < 2e-2
+    # bit-identical on a repeat (a key-split launch merges its halves in a fixed order)
+    e.attention_ex(tq, tk, tv, to, B, heads, Sq, Sk, d, C, C, C, C, 1.0 / math.sqrt(d), sdu.SDU_ATTN_Q_LOG2)
+    np.testing.assert_array_equal(to.numpy().astype(np.float32), got)
 
 
 @pytest.mark.parametrize("B", [4, 16])  # 128-key tiles (256 blocks), 64-key tiles (1024)
