@@ -43,6 +43,11 @@ static constexpr float kRescaleLog2 = 8.0f;  // lazy-rescale threshold (log2 uni
 // key-split shared-tile launches: pair counters at the head of the workspace (one per
 // query block, head and image; zero between launches), the partial slots after them
 static constexpr int kAttnMaxPairs = 16384;
+// Shared-tile launches stage V row-major and read it with transposing LDS reads (TRV),
+// except with 128-key tiles: per launch, with random operands, d40 at 9216 tokens B=2
+// -4.1%, at 4096 tokens B=16 -9%, d80 -10 to -13%, d160 at B=16 -10%, but d40 with
+// 128-key tiles (4096 tokens, B=2) +1.5%
+static constexpr bool kTRV = true;
 static constexpr int kAttnCounterFloats = kAttnMaxPairs;
 
 __device__ __forceinline__ int key_perm(int r) {
@@ -56,9 +61,41 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // P = 2^x as fp16 for the NSUB 32-key sub-tiles of scores s, x = s * c + nm (MODE 0) or
 // s (MODE 1), followed by O^T += V^T . P^T.  Returns the lane's sum of P when the row
 // sums do not come from the ones row of V^T (!LSUM).
-template <int NSUB, int MTD, bool LSUM, int MODE>
+// V^T fragment (the A operand of O^T += V^T . P^T) for dims t*32 + [0, 32) and keys
+// kofs + [0, 16): TR = false reads it from a transposed tile vt [dim][key] (one 16-byte
+// read); TR = true from a row-major tile vt [key][dim] with two ds_read_b64_tr_b16, whose
+// lane i of each 16-lane group receives element i of 4 consecutive rows: the lane's
+// address vlo (tr_lane_offset) selects 4 dims of one key row.
+typedef short short4v __attribute__((ext_vector_type(4)));
+template <bool TR>
+__device__ __forceinline__ half8 vt_frag(const f16* vt, int vstr, int t, int kofs_tile, int lrow, int lk, int vlo) {
+    if constexpr (TR) {
+        const f16* p = vt + kofs_tile * vstr + t * 32 + vlo;
+        const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)p);
+        const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) short4v*)(p + 4 * vstr));
+        const short r[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        half8 v;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = __builtin_bit_cast(f16, r[i]);
+        return v;
+    } else {
+        return *(const half8*)&vt[(t * 32 + lrow) * vstr + kofs_tile + lk];
+    }
+}
+
+// Lane offset (halves) of the transposing reads in a row-major V tile with row stride
+// vstr: 16-lane group g takes dims 16 (g % 2) + [0, 16) and keys 8 (g / 2) + [0, 8) of the
+// 32x32x16 A operand; its lane j reads key 8 (g / 2) + j / 4 (+ 4 for the second read),
+// dims 16 (g % 2) + 4 (j % 4) .. + 3.
+__device__ __forceinline__ int tr_lane_offset(int lane, int vstr) {
+    const int g = lane >> 4, j = lane & 15;
+    return (8 * (g >> 1) + (j >> 2)) * vstr + 16 * (g & 1) + 4 * (j & 3);
+}
+
+template <int NSUB, int MTD, bool LSUM, int MODE, bool TR = false>
 __device__ __forceinline__ float exp_pv(const floatx16 (&s)[NSUB], float c, float nm, floatx16 (&o)[MTD],
-                                        const f16* vt, int vstr, int lrow, int lk) {
+                                        const f16* vt, int vstr, int lrow, int lk, int vlo = 0) {
     float psum = 0.f;
 #pragma unroll
     for (int sub = 0; sub < NSUB; ++sub)
@@ -72,10 +109,9 @@ __device__ __forceinline__ float exp_pv(const floatx16 (&s)[NSUB], float c, floa
                 if (!LSUM) psum += p;
                 pf[i] = (f16)p;
             }
-            const int kofs = sub * 32 + st * 16 + lk;
 #pragma unroll
             for (int t = 0; t < MTD; ++t) {
-                const half8 vf = *(const half8*)&vt[(t * 32 + lrow) * vstr + kofs];
+                const half8 vf = vt_frag<TR>(vt, vstr, t, sub * 32 + st * 16, lrow, lk, vlo);
                 o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, o[t], 0, 0, 0);
             }
         }
@@ -112,10 +148,10 @@ __device__ __forceinline__ float mask_max(floatx16 (&s)[NSUB], int kvalid, int h
 // followed by O^T += V^T . P^T.  `kvalid` = number of valid keys in the tile for this
 // lane's query (< NSUB*32 only on the last tile, or below the causal limit; may be <= 0).
 // vt: V^T tile [dim][key] with row stride vstr.
-template <int NSUB, int MTD, bool LSUM>
+template <int NSUB, int MTD, bool LSUM, bool TR = false>
 __device__ __forceinline__ void softmax_pv(floatx16 (&s)[NSUB], int kvalid, float c, float& m_run,
                                            float& l_run, floatx16 (&o)[MTD], const f16* vt, int vstr,
-                                           int hl, int lrow, int lk) {
+                                           int hl, int lrow, int lk, int vlo = 0) {
     const float mxs = mask_max<NSUB>(s, kvalid, hl) * c;
     if (__ballot(mxs > m_run + kRescaleLog2)) {  // wave-uniform
         const float m_new = fmaxf(m_run, mxs);
@@ -128,7 +164,7 @@ __device__ __forceinline__ void softmax_pv(floatx16 (&s)[NSUB], int kvalid, floa
     // (a lane whose keys so far were all masked keeps m_run = -inf: subtract 0, so that
     // its masked scores give exp2(-inf) = 0 rather than exp2(-inf + inf))
     const float nm = m_run == -INFINITY ? 0.f : -m_run;
-    const float psum = exp_pv<NSUB, MTD, LSUM, 0>(s, c, nm, o, vt, vstr, lrow, lk);
+    const float psum = exp_pv<NSUB, MTD, LSUM, 0, TR>(s, c, nm, o, vt, vstr, lrow, lk, vlo);
     if (!LSUM) l_run += psum;
 }
 
@@ -189,14 +225,21 @@ __device__ __forceinline__ void vt_pad_rows(f16* vt, int vstr, int keys, int d, 
 // SPL: the keys are split in two parts at a.kpart (a multiple of KT), blockIdx.z = image * 2 +
 // part; each part's block stores its unnormalised O^T, reference and row-sum partial into a
 // workspace slot, and the pair's second block to finish merges both (see the end).
-template <int KS, int MTD, int NWAVE, bool LSUM, int KT = 64, bool OFS = false, bool SPL = false>
+// TRV: V is staged row-major ([key][dim], 16-byte stores as K) and the PV A operand is
+// read with transposing LDS reads (vt_frag) instead of staging V^T.
+template <int KS, int MTD, int NWAVE, bool LSUM, int KT = 64, bool OFS = false, bool SPL = false,
+          bool TRV = false>
 __global__ __launch_bounds__(NWAVE * 64) void attn_kernel(AttnArgs a) {
-    constexpr int VSTR = KT + 8;  // Vt row stride (halves)
+    // V tile: V^T [dim][key] with row stride KT + 8, or (TRV) V [key][dim] with a row stride
+    // of 16 (mod 64) halves: the four key rows one 16-lane transposing read touches then
+    // fall on distinct banks
+    constexpr int VSTR = TRV ? ((MTD * 32 - 16 + 63) / 64) * 64 + 16 : KT + 8;
+    constexpr int VTILE = TRV ? KT * VSTR : MTD * 32 * VSTR;
     constexpr int NSUB = KT / 32;
     constexpr int KSTR = KS * 16 + 8;  // K row stride (halves)
     constexpr int NTH = NWAVE * 64;
     __shared__ __attribute__((aligned(16))) f16 Ks[2][KT * KSTR];
-    __shared__ __attribute__((aligned(16))) f16 Vt[2][MTD * 32 * VSTR];
+    __shared__ __attribute__((aligned(16))) f16 Vt[2][VTILE];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = blockIdx.y;
@@ -213,8 +256,18 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_kernel(AttnArgs a) {
         f16* row = &Ks[i / KT][(i % KT) * KSTR];
         for (int x = d; x < KS * 16; ++x) row[x] = (f16)((OFS && x == d) ? 1.f : 0.f);
     }
-    vt_pad_rows<MTD, LSUM>(Vt[0], VSTR, KT, d, tid, NTH);
-    vt_pad_rows<MTD, LSUM>(Vt[1], VSTR, KT, d, tid, NTH);
+    if constexpr (TRV) {
+        // dims [d, MTD*32) of every key row: zero, the last one 1 when LSUM (row sums)
+        const int pad = MTD * 32 - d;
+        for (int i = tid; i < 2 * KT * pad; i += NTH) {
+            const int bf = i / (KT * pad), r = i % (KT * pad), key = r / pad, dim = d + r % pad;
+            Vt[bf][key * VSTR + dim] = (f16)((LSUM && dim == MTD * 32 - 1) ? 1.f : 0.f);
+        }
+    } else {
+        vt_pad_rows<MTD, LSUM>(Vt[0], VSTR, KT, d, tid, NTH);
+        vt_pad_rows<MTD, LSUM>(Vt[1], VSTR, KT, d, tid, NTH);
+    }
+    const int vlo = TRV ? tr_lane_offset(lane, VSTR) : 0;
 
     // Q fragment (B operand of S^T = K Q^T): lane holds Q[q0+lrow][ks*16+lk .. +7]
     half8 qf[KS];
@@ -250,8 +303,10 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_kernel(AttnArgs a) {
     // the transposed store to V^T [dim][key] is 8 ds_write_b64 (4 keys of one dim each)
     // instead of 32 two-byte stores.
     constexpr int MAXCH = (KT * KS * 2 + NTH - 1) / NTH;        // >= KT*d/8/NTH
-    constexpr int MAXU = (KT / 4 * KS * 2 + NTH - 1) / NTH;     // >= (KT/4)*(d/8)/NTH
-    uint4 rk[MAXCH], rv[MAXU][4];
+    // V per thread and step: TRV, MAXCH 16-byte chunks (as K); else MAXU units of 4 keys
+    constexpr int MAXU = TRV ? MAXCH : (KT / 4 * KS * 2 + NTH - 1) / NTH;  // >= (KT/4)*(d/8)/NTH
+    constexpr int VLD = TRV ? 1 : 4;                            // 16-byte loads per unit
+    uint4 rk[MAXCH], rv[MAXU][VLD];
     const int nchunk = KT * dch, nunit = KT / 4 * dch;
     uint32_t kvo[MAXCH], vvo[MAXU];
     int sto[MAXCH];  // LDS position of the K chunk: key << 16 | dc*8; -1: no chunk
@@ -267,10 +322,17 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_kernel(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < MAXU; ++i) {
         const int u = tid + i * NTH;
-        const int kq = u / dch, dc = u - kq * dch;
-        const bool ok = u < nunit;
-        vvo[i] = ok ? (uint32_t)((4 * kq * a.ldv + dc * 8) * 2) : 0x80000000u;
-        vto[i] = ok ? 4 * kq * 65536 + dc * 8 : -1;
+        if constexpr (TRV) {
+            const int key = u / dch, dc = u - key * dch;
+            const bool ok = u < nchunk;
+            vvo[i] = ok ? (uint32_t)((key * a.ldv + dc * 8) * 2) : 0x80000000u;
+            vto[i] = ok ? key * VSTR + dc * 8 : -1;  // LDS offset (halves)
+        } else {
+            const int kq = u / dch, dc = u - kq * dch;
+            const bool ok = u < nunit;
+            vvo[i] = ok ? (uint32_t)((4 * kq * a.ldv + dc * 8) * 2) : 0x80000000u;
+            vto[i] = ok ? 4 * kq * 65536 + dc * 8 : -1;
+        }
     }
     auto load_kv = [&](int kb) {
         const uint32_t ko = (uint32_t)(kb * a.ldk * 2), vo = (uint32_t)(kb * a.ldv * 2);
@@ -281,7 +343,7 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_kernel(AttnArgs a) {
 #pragma unroll
         for (int i = 0; i < MAXU; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < VLD; ++j)
                 rv[i][j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
                                                          rsv, vvo[i] + vo + j * vrow, 0, 0));
     };
@@ -291,12 +353,14 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_kernel(AttnArgs a) {
             if (sto[i] >= 0) *(uint4*)&Ks[buf][(sto[i] >> 16) * KSTR + (sto[i] & 0xffff)] = rk[i];
 #pragma unroll
         for (int i = 0; i < MAXU; ++i) {
-            if (vto[i] >= 0) {
+            if constexpr (TRV) {
+                if (vto[i] >= 0) *(uint4*)&Vt[buf][vto[i]] = rv[i][0];
+            } else if (vto[i] >= 0) {
                 const int key = vto[i] >> 16, c8 = vto[i] & 0xffff;
                 const uint32_t* w0 = (const uint32_t*)&rv[i][0];
-                const uint32_t* w1 = (const uint32_t*)&rv[i][1];
-                const uint32_t* w2 = (const uint32_t*)&rv[i][2];
-                const uint32_t* w3 = (const uint32_t*)&rv[i][3];
+                const uint32_t* w1 = (const uint32_t*)&rv[i][VLD > 1 ? 1 : 0];
+                const uint32_t* w2 = (const uint32_t*)&rv[i][VLD > 2 ? 2 : 0];
+                const uint32_t* w3 = (const uint32_t*)&rv[i][VLD > 3 ? 3 : 0];
 #pragma unroll
                 for (int e2 = 0; e2 < 4; ++e2) {
                     // dims 2*e2 (low halves) and 2*e2+1 (high halves) of the 4 keys
@@ -355,10 +419,10 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_kernel(AttnArgs a) {
                 qk();
                 mask_tile<NSUB>(s, kvalid, hl);
             }
-            const float psum = exp_pv<NSUB, MTD, LSUM, 1>(s, 1.f, 0.f, o, Vt[buf], VSTR, lrow, lk);
+            const float psum = exp_pv<NSUB, MTD, LSUM, 1, TRV>(s, 1.f, 0.f, o, Vt[buf], VSTR, lrow, lk, vlo);
             if (!LSUM) l_run += psum;
         } else {
-            softmax_pv<NSUB, MTD, LSUM>(s, kvalid, c, m_run, l_run, o, Vt[buf], VSTR, hl, lrow, lk);
+            softmax_pv<NSUB, MTD, LSUM, TRV>(s, kvalid, c, m_run, l_run, o, Vt[buf], VSTR, hl, lrow, lk, vlo);
         }
         __builtin_amdgcn_s_setprio(0);
         if (it + 1 < nt) store_kv(buf ^ 1);
@@ -676,8 +740,8 @@ static AttnPlan attn_plan(const AttnArgs& a) {
         // rounds of 768 blocks; measured 1.75 round-times)
         if (p.nw == 4 && !p.kt128 && a.Sk > 64 && (long)p.grid.x * bh <= kAttnMaxPairs) {
             const long nblk = (long)p.grid.x * bh;
-            const int slots = p.ofs ? resident_blocks<KS, MTD, LSUM, true>(attn_kernel<KS, MTD, 4, LSUM, 64, true>, 256)
-                                    : resident_blocks<KS, MTD, LSUM, false>(attn_kernel<KS, MTD, 4, LSUM>, 256);
+            const int slots = p.ofs ? resident_blocks<KS, MTD, LSUM, true>(attn_kernel<KS, MTD, 4, LSUM, 64, true, false, kTRV>, 256)
+                                    : resident_blocks<KS, MTD, LSUM, false>(attn_kernel<KS, MTD, 4, LSUM, 64, false, false, kTRV>, 256);
             if (slots > 0) {
                 auto rounds = [&](double r) { const double f = floor(r); return f + (r > f ? 0.75 : 0.0); };
                 p.spl = rounds(2.0 * nblk / slots) * 0.5 + 0.05 < 0.9 * rounds((double)nblk / slots);
@@ -714,8 +778,10 @@ static void launch_cfg(const AttnArgs& a0, hipStream_t s) {
     char name[48];
     if (p.shared) {
         const bool spl = p.spl && a.ws;
-        snprintf(name, sizeof name, "attn_kernel<%d,%d,%d,%d,%d%s%s>", KS, MTD, p.nw, (int)LSUM, p.kt128 ? 128 : 64,
-                 p.ofs || spl ? (p.ofs ? ",1" : ",0") : "", spl ? ",1" : "");
+        const bool trv = kTRV && !p.kt128;
+        snprintf(name, sizeof name, "attn_kernel<%d,%d,%d,%d,%d%s%s%s>", KS, MTD, p.nw, (int)LSUM, p.kt128 ? 128 : 64,
+                 p.ofs || spl || trv ? (p.ofs ? ",1" : ",0") : "", spl || trv ? (spl ? ",1" : ",0") : "",
+                 trv ? ",1" : "");
         constexpr int KTB = KS == 3 ? 128 : 64;
         dim3 grid = p.grid;
         if (spl) {
@@ -723,13 +789,15 @@ static void launch_cfg(const AttnArgs& a0, hipStream_t s) {
             grid.z *= 2;
         }
         launch_timed(name, flops, bytes, [&] {
-            if (p.nw == 8) SDU_LAUNCH((attn_kernel<KS, MTD, 8, LSUM>), grid, dim3(512), 0, s, a);
-            else if (KS == 3 && p.kt128 && p.ofs) SDU_LAUNCH((attn_kernel<KS, MTD, 4, LSUM, KTB, true>), grid, dim3(256), 0, s, a);
-            else if (KS == 3 && p.kt128) SDU_LAUNCH((attn_kernel<KS, MTD, 4, LSUM, KTB>), grid, dim3(256), 0, s, a);
-            else if (spl && p.ofs) SDU_LAUNCH((attn_kernel<KS, MTD, 4, LSUM, 64, true, true>), grid, dim3(256), 0, s, a);
-            else if (spl) SDU_LAUNCH((attn_kernel<KS, MTD, 4, LSUM, 64, false, true>), grid, dim3(256), 0, s, a);
-            else if (p.ofs) SDU_LAUNCH((attn_kernel<KS, MTD, 4, LSUM, 64, true>), grid, dim3(256), 0, s, a);
-            else SDU_LAUNCH((attn_kernel<KS, MTD, 4, LSUM>), grid, dim3(256), 0, s, a);
+            if (p.nw == 8) SDU_LAUNCH((attn_kernel<KS, MTD, 8, LSUM, 64, false, false, kTRV>), grid, dim3(512), 0, s, a);
+            else if (KS == 3 && p.kt128 && p.ofs)
+                SDU_LAUNCH((attn_kernel<KS, MTD, 4, LSUM, KTB, true>), grid, dim3(256), 0, s, a);
+            else if (KS == 3 && p.kt128)
+                SDU_LAUNCH((attn_kernel<KS, MTD, 4, LSUM, KTB>), grid, dim3(256), 0, s, a);
+            else if (spl && p.ofs) SDU_LAUNCH((attn_kernel<KS, MTD, 4, LSUM, 64, true, true, kTRV>), grid, dim3(256), 0, s, a);
+            else if (spl) SDU_LAUNCH((attn_kernel<KS, MTD, 4, LSUM, 64, false, true, kTRV>), grid, dim3(256), 0, s, a);
+            else if (p.ofs) SDU_LAUNCH((attn_kernel<KS, MTD, 4, LSUM, 64, true, false, kTRV>), grid, dim3(256), 0, s, a);
+            else SDU_LAUNCH((attn_kernel<KS, MTD, 4, LSUM, 64, false, false, kTRV>), grid, dim3(256), 0, s, a);
         });
         return;
     }
