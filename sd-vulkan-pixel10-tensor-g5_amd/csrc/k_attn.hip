@@ -514,7 +514,10 @@ static constexpr int VSTRS = KTS + 8;  // per-wave Vt row stride (halves)
 
 template <int MTD, int NSPLIT>
 struct SplitSmem {
-    static constexpr int vt_bytes = NSPLIT * MTD * 32 * VSTRS * 2;
+    // per-wave V tile: V^T [MTD*32][VSTRS], or (TRV) V [KTS][trv_stride(MTD)]
+    static constexpr int trv_stride = ((MTD * 32 - 16 + 63) / 64) * 64 + 16;
+    static constexpr int vt_elems = kTRV ? KTS * trv_stride : MTD * 32 * VSTRS;
+    static constexpr int vt_bytes = NSPLIT * vt_elems * 2;
     static constexpr int comb_bytes = NSPLIT * (MTD * 32 * 32 + 64) * 4;
     static constexpr int bytes = vt_bytes > comb_bytes ? vt_bytes : comb_bytes;
 };
@@ -537,9 +540,20 @@ __global__ __launch_bounds__(NSPLIT * 64) void attn_split_kernel(AttnArgs a) {
     const int q0 = blockIdx.x * 32;
     const int lrow = lane & 31, hl = lane >> 5, lk = hl * 8;
     const float c = a.q_log2 ? 1.f : a.scale * 1.4426950408889634f;
-    f16* vt = (f16*)smem + wave * (MTD * 32 * VSTRS);
+    constexpr int VS = kTRV ? SplitSmem<MTD, NSPLIT>::trv_stride : VSTRS;  // V tile row stride
+    f16* vt = (f16*)smem + wave * SplitSmem<MTD, NSPLIT>::vt_elems;
 
-    vt_pad_rows<MTD, LSUM>(vt, VSTRS, KTS, d, lane, 64);
+    if constexpr (kTRV) {
+        // dims [d, MTD*32) of every key row: zero, the last one 1 when LSUM (row sums)
+        const int pad = MTD * 32 - d;
+        for (int i = lane; i < KTS * pad; i += 64) {
+            const int key = i / pad, dim = d + i % pad;
+            vt[key * VS + dim] = (f16)((LSUM && dim == MTD * 32 - 1) ? 1.f : 0.f);
+        }
+    } else {
+        vt_pad_rows<MTD, LSUM>(vt, VSTRS, KTS, d, lane, 64);
+    }
+    const int vlo = kTRV ? tr_lane_offset(lane, VS) : 0;
 
     half8 qf[KS];
     {
@@ -563,10 +577,13 @@ __global__ __launch_bounds__(NSPLIT * 64) void attn_split_kernel(AttnArgs a) {
     const f16* vbase = a.v + (int64_t)b * a.Sk * a.ldv + (int64_t)h * d;
     // V: one unit = the same 8 dims of 4 consecutive keys per lane, so that the
     // transposed store to V^T [dim][key] is 8 ds_write_b64 (4 keys of one dim each)
-    constexpr int MAXU = (KTS / 4 * KS * 2 + 63) / 64;  // >= (KTS/4)*(d/8)/64
-    const int nunit = KTS / 4 * dch;
+    // V per lane and tile: (TRV) MAXU 16-byte chunks (8 dims of one key), else MAXU units of
+    // the same 8 dims of 4 consecutive keys
+    constexpr int MAXU = kTRV ? (KTS * KS * 2 + 63) / 64 : (KTS / 4 * KS * 2 + 63) / 64;
+    constexpr int VLD = kTRV ? 1 : 4;
+    const int nunit = kTRV ? KTS * dch : KTS / 4 * dch;
     half8 kf[KS];
-    uint4 rv[MAXU][4];
+    uint4 rv[MAXU][VLD];
 
     auto load = [&](int kb) {
         const int key = kb + key_perm(lrow);
@@ -582,8 +599,8 @@ __global__ __launch_bounds__(NSPLIT * 64) void attn_split_kernel(AttnArgs a) {
             const int u = lane + i * 64;
             const int kq = u / dch, dc = u - kq * dch;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int key = kb + 4 * kq + j;
+            for (int j = 0; j < VLD; ++j) {
+                const int key = kb + (kTRV ? kq : 4 * kq + j);
                 uint4 vv = make_uint4(0, 0, 0, 0);
                 if (u < nunit && key < a.Sk) vv = *(const uint4*)(vbase + (int64_t)key * a.ldv + dc * 8);
                 rv[i][j] = vv;
@@ -594,12 +611,15 @@ __global__ __launch_bounds__(NSPLIT * 64) void attn_split_kernel(AttnArgs a) {
 #pragma unroll
         for (int i = 0; i < MAXU; ++i) {
             const int u = lane + i * 64;
-            if (u < nunit) {
+            if (kTRV) {
+                const int kq = u / dch;
+                if (u < nunit) *(uint4*)&vt[kq * VS + (u - kq * dch) * 8] = rv[i][0];
+            } else if (u < nunit) {
                 const int kq = u / dch, c8 = (u - kq * dch) * 8, key = 4 * kq;
                 const uint32_t* w0 = (const uint32_t*)&rv[i][0];
-                const uint32_t* w1 = (const uint32_t*)&rv[i][1];
-                const uint32_t* w2 = (const uint32_t*)&rv[i][2];
-                const uint32_t* w3 = (const uint32_t*)&rv[i][3];
+                const uint32_t* w1 = (const uint32_t*)&rv[i][VLD > 1 ? 1 : 0];
+                const uint32_t* w2 = (const uint32_t*)&rv[i][VLD > 2 ? 2 : 0];
+                const uint32_t* w3 = (const uint32_t*)&rv[i][VLD > 3 ? 3 : 0];
 #pragma unroll
                 for (int e2 = 0; e2 < 4; ++e2) {
                     // dims 2*e2 (low halves) and 2*e2+1 (high halves) of the 4 keys
@@ -633,7 +653,7 @@ __global__ __launch_bounds__(NSPLIT * 64) void attn_split_kernel(AttnArgs a) {
         __builtin_amdgcn_s_setprio(1);
         // causal: query q0 + lrow sees keys up to itself
         const int kv = a.causal ? min(KTS, min(a.Sk, q0 + lrow + 1) - kb) : min(KTS, a.Sk - kb);
-        softmax_pv<1, MTD, LSUM>(s, kv, c, m_run, l_run, o, vt, VSTRS, hl, lrow, lk);
+        softmax_pv<1, MTD, LSUM, kTRV>(s, kv, c, m_run, l_run, o, vt, VS, hl, lrow, lk, vlo);
         __builtin_amdgcn_s_setprio(0);
         __builtin_amdgcn_wave_barrier();
     }
