@@ -297,10 +297,36 @@ def main():
     ap.add_argument("--ref-ops", action="store_true",
                     help="only time the reference's micro-benchmark shapes (REF_OPS), print one JSON "
                          "line and exit")
+    ap.add_argument("--only-vae", action="store_true",
+                    help="only time `steps` full-VAE decodes of one 64x64 latent (seeded weights; "
+                         "marked timed_vae_64x64, for profiler runs), print one JSON line and exit")
     args = ap.parse_args()
     if args.ref_ops:
         import sdu
         print(json.dumps({"reference_bench_ops": time_reference_ops(sdu)}), flush=True)
+        return
+    if args.only_vae:
+        import numpy as np
+        import torch
+        import sdu
+        eng = sdu.Engine(flags=sdu.SDU_INIT_NO_WEIGHTS)
+        eng.vae_init(seed=7)
+        d_lat = eng.upload(np.random.default_rng(0).standard_normal((1, 4, 64, 64)).astype(np.float32))
+        d_img = eng.tensor((1, 3, 512, 512), sdu.SDU_F32)
+        for _ in range(args.warmup):
+            eng.vae_decode_device(d_lat.ptr, 1, 64, 64, d_img.ptr)
+        eng.sync()
+        torch.cuda.nvtx.range_push("timed_vae_64x64")
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            eng.vae_decode_device(d_lat.ptr, 1, 64, 64, d_img.ptr)
+        eng.sync()
+        ms = (time.perf_counter() - t0) / args.steps * 1e3
+        torch.cuda.nvtx.range_pop()
+        eng.release()
+        flop = vae_decode_flop(64, 64)
+        print(json.dumps({"only": "vae_64x64", "ms_per_decode": round(ms, 4), "steps": args.steps,
+                          "warmup": args.warmup, "tflops": round(flop / ms / 1e9, 1)}), flush=True)
         return
     if args.copy_probe:
         import torch
