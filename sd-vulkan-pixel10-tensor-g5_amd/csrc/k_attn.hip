@@ -799,9 +799,8 @@ static void launch_cfg(const AttnArgs& a0, hipStream_t s) {
     if (p.shared) {
         const bool spl = p.spl && a.ws;
         const bool trv = kTRV && !p.kt128;
-        snprintf(name, sizeof name, "attn_kernel<%d,%d,%d,%d,%d%s%s%s>", KS, MTD, p.nw, (int)LSUM, p.kt128 ? 128 : 64,
-                 p.ofs || spl || trv ? (p.ofs ? ",1" : ",0") : "", spl || trv ? (spl ? ",1" : ",0") : "",
-                 trv ? ",1" : "");
+        snprintf(name, sizeof name, "attn_kernel<%d,%d,%d,%d,%d,%d,%d,%d>", KS, MTD, p.nw, (int)LSUM, p.kt128 ? 128 : 64,
+                 (int)p.ofs, (int)spl, (int)trv);
         constexpr int KTB = KS == 3 ? 128 : 64;
         dim3 grid = p.grid;
         if (spl) {
