@@ -383,10 +383,19 @@ void gemm_kernel(GemmArgs a) {
     const __amdgpu_buffer_rsrc_t rsA3 = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(a.A3 ? a.A3 : a.A), (short)0, a.A3 ? a.M * a.lda3 * 2 : 0, 0x00020000);
     // conv fast path: each K tile lies inside one tap (Cin % BKT == 0) and the input
-    // is not upsampled, so the tap offset is one scalar per tile
+    // is not upsampled, so the tap offset is one scalar per tile.  The K tiles of the
+    // conv part go channel-chunk-major: the 9 taps of one BKT-channel chunk back to back
+    // (virtual tile v = chunk * 9 + tap, real K offset tap * Cin + chunk * BKT), so the
+    // block's input pixels (its rows and their halo) are re-read for the next tap while
+    // that chunk is still in L2, rather than after a sweep over all Cin channels.  A
+    // split-K block takes a contiguous range of virtual tiles.
     const bool conv_fast = AM == A_CONV3 && a.Cin % BKT == 0 && !a.upsample;
     int tap_next = 0, c_next = 0;  // tap / channel of the next tile issued (fast path)
-    if (conv_fast) { tap_next = kbeg / a.Cin; c_next = kbeg - tap_next * a.Cin; }
+    if (conv_fast) {
+        const int v0 = kbeg / BKT, chunk = v0 / 9;
+        tap_next = v0 - chunk * 9;
+        c_next = chunk * BKT;
+    }
 
     auto dma = [&](const f16* src, f16* dst) __attribute__((always_inline)) {
         __builtin_amdgcn_global_load_lds((const void*)src, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
@@ -397,6 +406,7 @@ void gemm_kernel(GemmArgs a) {
     auto issue = [&](int kt, int stage) __attribute__((always_inline)) {
         const int k0 = kbeg + kt * BKT;
         const bool tail = k0 + BKT > kend;  // partial K tile
+        int kw = k0;                        // the tile's real K offset (weights)
         f16* sA = smem + stage * STAGE;
         f16* sB = sA + MT * BKT;
         if (DENSE) {
@@ -430,8 +440,8 @@ void gemm_kernel(GemmArgs a) {
         } else if (conv_fast) {
             const int tap = tap_next, ky = tap / 3, kx = tap - ky * 3;
             const int toff = (ky * a.Win + kx) * a.Cin + c_next;
-            c_next += BKT;
-            if (c_next == a.Cin) { c_next = 0; ++tap_next; }
+            kw = tap * a.Cin + c_next;
+            if (++tap_next == 9) { tap_next = 0; c_next += BKT; }
 #pragma unroll
             for (int i = 0; i < AI; ++i) {
                 const bool ok = ((a_vm[i] >> tap) & 1) && !(tail && k0 + a_c[i] >= kend);
@@ -452,7 +462,7 @@ void gemm_kernel(GemmArgs a) {
         }
         if (!tail) {
 #pragma unroll
-            for (int i = 0; i < BI; ++i) bdma(rsB, voB[i], k0 * 2, sB + (i * NW + wave) * RPI * BKT);
+            for (int i = 0; i < BI; ++i) bdma(rsB, voB[i], kw * 2, sB + (i * NW + wave) * RPI * BKT);
         } else {
 #pragma unroll
             for (int i = 0; i < BI; ++i)
