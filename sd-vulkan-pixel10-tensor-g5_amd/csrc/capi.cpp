@@ -246,7 +246,8 @@ int sdu_set_weight(sdu_ctx* ctx, const char* name, const float* data, int64_t nu
         };
         static const char* const kFoldSources[] = {
             ".ff.net.2.weight", ".ff.net.2.bias", ".proj_out.weight", ".proj_out.bias",    // FF out + proj_out
-            ".conv2.weight", ".conv2.bias", ".conv_shortcut.weight", ".conv_shortcut.bias"};  // resnet shortcut
+            ".conv2.weight", ".conv2.bias", ".conv_shortcut.weight", ".conv_shortcut.bias",   // resnet shortcut
+            ".upsamplers.0.conv.weight"};                                                     // sub-pixel weights
         // LayerNorm folds (a resnet's norm1 / norm2 are GroupNorms, not folded)
         static const char* const kLnFoldSources[] = {
             ".norm1.weight", ".norm1.bias", ".attn1.to_q.weight", ".attn1.to_k.weight", ".attn1.to_v.weight",

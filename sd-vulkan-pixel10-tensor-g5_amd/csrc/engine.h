@@ -65,6 +65,14 @@ struct ResDesc {
 static const int kUnetHeads = 8;
 inline float attn_qscale(int C) { return 1.4426950408889634f / sqrtf((float)(C / kUnetHeads)); }
 
+// A 3x3 conv after a 2x nearest upsampling, with its sub-pixel weights (GemmArgs::subpix;
+// fold_weights): [4 phases][C][2][2][C]
+struct UpDesc {
+    std::string pf;  // the conv's prefix
+    int c;
+    f16* w4 = nullptr;
+};
+
 struct XfDesc {
     std::string pf;
     int c;
@@ -111,6 +119,8 @@ struct AuxNet {
     f16* w2sc[2] = {nullptr, nullptr};
     f16* b2sc[2] = {nullptr, nullptr};
     float* b_attn_out = nullptr;
+    // VAE / TAESD: sub-pixel weights of the convs after each 2x upsampling (GemmArgs::subpix)
+    f16* w4[3] = {nullptr, nullptr, nullptr};
     int add(const std::string& name, std::vector<int64_t> shape, int kind, int layout = GL_PLAIN, int ci_pad = 0,
             bool follows = false);
     const WeightRec* w(const std::string& name) const {
@@ -144,6 +154,7 @@ struct Ctx {
     int kv_total = 0;
     std::vector<ResDesc> resnets;
     std::vector<XfDesc> xfs;
+    std::vector<UpDesc> ups;
     std::map<std::string, int> res_by_pf, xf_by_pf;
 
     // op-level tensors and per-shape forward state

@@ -305,6 +305,11 @@ void gemm_kernel(GemmArgs a) {
         tn = bid - tm * tiles_n;
     }
     const int m0 = tm * MT, n0 = tn * NT;
+    // sub-pixel conv (GemmArgs::subpix): the tile's phase (a tile never straddles two)
+    // and the first GEMM row of that phase
+    const bool subpix = AM == A_CONV3 && a.subpix;
+    const int sp_rows = a.M >> 2;
+    const int sp_ph = subpix ? m0 / sp_rows : 0, sp_base = sp_ph * sp_rows;
 
     const int kbeg = blockIdx.z * a.k_per_split;
     const int kend = min(a.K, kbeg + a.k_per_split);
@@ -328,14 +333,14 @@ void gemm_kernel(GemmArgs a) {
     const f16* zero = (const f16*)g_zero_page;
     constexpr uint32_t kOOB = 0x80000000u;
     const __amdgpu_buffer_rsrc_t rsB =
-        __builtin_amdgcn_make_buffer_rsrc((void*)a.Wt, (short)0, a.N * a.K * 2, 0x00020000);
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.Wt, (short)0, (subpix ? 4 : 1) * a.N * a.K * 2, 0x00020000);
     uint32_t voB[BI];
     int b_c[BI];
 #pragma unroll
     for (int i = 0; i < BI; ++i) {
         const int row = (i * NW + wave) * RPI + lr;
         b_c[i] = (pchunk ^ lds_swizzle<BKT>(row)) * 8;
-        voB[i] = (uint32_t)((min(n0 + row, a.N - 1) * a.K + b_c[i]) * 2);
+        voB[i] = (uint32_t)(((sp_ph * a.N + min(n0 + row, a.N - 1)) * a.K + b_c[i]) * 2);
     }
     int a_c[AI];          // element offset of the lane's chunk within the K tile
     int a_m[AI];          // dense: row (clamped)
@@ -357,6 +362,23 @@ void gemm_kernel(GemmArgs a) {
         } else {
             voA2[i] = a.A2 ? (uint32_t)((m * a.lda2 + a_c[i]) * 2) : 0u;
             voA3[i] = a.A3 ? (uint32_t)((m * a.lda3 + a_c[i]) * 2) : 0u;
+            if (subpix) {
+                // input pixel (iy, ix) of phase (py, px): 2x2 taps at rows iy + py - 1 + ty,
+                // columns ix + px - 1 + tx
+                const int hwi = a.Hin * a.Win, q = m - sp_base;
+                const int bb = q / hwi, r = q - bb * hwi, iy = r / a.Win, ix = r - iy * a.Win;
+                const int y0 = iy + (sp_ph >> 1) - 1, x0 = ix + (sp_ph & 1) - 1;
+                a_b[i] = bb; a_oy[i] = iy; a_ox[i] = ix;
+                a_off[i] = ((bb * a.Hin + y0) * a.Win + x0) * a.Cin + a_c[i];
+                int vm = 0;
+#pragma unroll
+                for (int ty = 0; ty < 2; ++ty)
+#pragma unroll
+                    for (int tx = 0; tx < 2; ++tx)
+                        if (y0 + ty >= 0 && y0 + ty < a.Hin && x0 + tx >= 0 && x0 + tx < a.Win) vm |= 1 << (ty * 2 + tx);
+                a_vm[i] = vm;
+                continue;
+            }
             const int hw = a.Ho * a.Wo;
             const int bb = m / hw, p = m - bb * hw;
             const int oy = p / a.Wo, ox = p - oy * a.Wo;
@@ -390,10 +412,11 @@ void gemm_kernel(GemmArgs a) {
     // that chunk is still in L2, rather than after a sweep over all Cin channels.  A
     // split-K block takes a contiguous range of virtual tiles.
     const bool conv_fast = AM == A_CONV3 && a.Cin % BKT == 0 && !a.upsample;
+    const int ntap = subpix ? 4 : 9;  // 3x3 taps, or the sub-pixel form's 2x2
     int tap_next = 0, c_next = 0;  // tap / channel of the next tile issued (fast path)
     if (conv_fast) {
-        const int v0 = kbeg / BKT, chunk = v0 / 9;
-        tap_next = v0 - chunk * 9;
+        const int v0 = kbeg / BKT, chunk = v0 / ntap;
+        tap_next = v0 - chunk * ntap;
         c_next = chunk * BKT;
     }
 
@@ -438,10 +461,10 @@ void gemm_kernel(GemmArgs a) {
                 for (int i = 0; i < AI; ++i) bdma(rsA3, voA3[i], (k0 - a.K2) * 2, sA + (i * NW + wave) * RPI * BKT);
             }
         } else if (conv_fast) {
-            const int tap = tap_next, ky = tap / 3, kx = tap - ky * 3;
+            const int tap = tap_next, ky = subpix ? tap >> 1 : tap / 3, kx = tap - ky * (subpix ? 2 : 3);
             const int toff = (ky * a.Win + kx) * a.Cin + c_next;
             kw = tap * a.Cin + c_next;
-            if (++tap_next == 9) { tap_next = 0; c_next += BKT; }
+            if (++tap_next == ntap) { tap_next = 0; c_next += BKT; }
 #pragma unroll
             for (int i = 0; i < AI; ++i) {
                 const bool ok = ((a_vm[i] >> tap) & 1) && !(tail && k0 + a_c[i] >= kend);
@@ -814,7 +837,8 @@ void gemm_kernel(GemmArgs a) {
     // per-channel output statistics (GroupNorm of the consumer): this thread's 8
     // columns over its rows, for the tile's first image (slot 0) and the next (slot 1)
     const bool do_st = a.stats != nullptr && !narrow;
-    const int st_b0 = do_st ? m0 / a.stats_hw : 0;
+    // (sub-pixel conv: statistics rows counted within the phase, stats_hw = Hin * Win)
+    const int st_b0 = do_st ? (m0 - sp_base) / a.stats_hw : 0;
     float st[2][2][8];
 #pragma unroll
     for (int sl = 0; sl < 2; ++sl)
@@ -917,7 +941,13 @@ void gemm_kernel(GemmArgs a) {
                 f16* oh = (f16*)&o;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) oh[e] = (f16)v[e];
-                *(uint4*)((f16*)a.C + (int64_t)m * a.ldc + nout) = o;
+                int mo = m;  // output row (sub-pixel conv: the phase's pixel in the upsampled image)
+                if (subpix) {
+                    const int hwi = a.Hin * a.Win, q = m - sp_base;
+                    const int bb = q / hwi, r = q - bb * hwi, iy = r / a.Win, ix = r - iy * a.Win;
+                    mo = (bb * a.Ho + 2 * iy + (sp_ph >> 1)) * a.Wo + 2 * ix + (sp_ph & 1);
+                }
+                *(uint4*)((f16*)a.C + (int64_t)mo * a.ldc + nout) = o;
                 if (do_rs) {
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
@@ -927,7 +957,7 @@ void gemm_kernel(GemmArgs a) {
                     }
                 }
                 if (do_st) {
-                    const bool s1 = m / a.stats_hw != st_b0;
+                    const bool s1 = (m - sp_base) / a.stats_hw != st_b0;
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         const float f = (float)oh[e];
@@ -942,7 +972,7 @@ void gemm_kernel(GemmArgs a) {
             }
         }
     }
-    if (do_st) stats_flush<NTH, NT / 8>(a, st, st_b0, min(a.M, m0 + MT) - 1, n0, (float*)smem);
+    if (do_st) stats_flush<NTH, NT / 8>(a, st, st_b0, min(a.M, m0 + MT) - 1 - sp_base, n0, (float*)smem);
     if (do_rs) {
         // the cpr threads of a row are consecutive lanes, each 8 of them one 64-column
         // group: add their partial sums; the first of the 8 stores the group's partial
@@ -1121,7 +1151,9 @@ void plan(const GemmArgs& a, int& ci, int& splits, int& kps, bool& fix) {
         // the 128x128 tile at K = 1280 (M = 1152, N = 3840: 27.8 against 25.7 us), which
         // the model does not see
         if (a.ln_part && g.mt == 64) continue;
-        if (a.stats && !stats_tile_ok(g.mt, a.stats_hw)) continue;
+        // (sub-pixel conv: whole phases per tile; statistics images of Hin * Win rows)
+        if (a.subpix && (a.M >> 2) % g.mt) continue;
+        if (a.stats && !stats_tile_ok(g.mt, a.subpix ? a.Hin * a.Win : a.stats_hw)) continue;
         const int tiles = ceil_div(a.M, g.mt) * ceil_div(a.N, g.nt);
         static const int cand[] = {1, 2, 3, 4, 6, 8, 12, 16, 24, 32};
         for (int s : cand) {
@@ -1141,7 +1173,7 @@ void plan(const GemmArgs& a, int& ci, int& splits, int& kps, bool& fix) {
             if (se > 1) {
                 const double part = (double)se * a.M * a.N * 8.0 / 20.0e12;
                 // (with output statistics only the in-kernel sum: the reduce keeps none)
-                const double t_red = (a.stats || a.row_part || a.ln_part) ? 1e30 : part + 5.5e-6;
+                const double t_red = (a.stats || a.row_part || a.ln_part || a.subpix) ? 1e30 : part + 5.5e-6;
                 const int rounds = ceil_div(se, g.spr);
                 const double t_fix = tiles <= kMaxSplitTiles ? part + kFixBase + kFixRound * rounds : 1e30;
                 fx = t_fix < t_red;
@@ -1216,6 +1248,14 @@ hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s) {
         return hipErrorInvalidValue;
     if (a.row_part && (a.out_mode != OUT_F16 || a.geglu || (a.N & 63) || (splits > 1 && !fix)))
         return hipErrorInvalidValue;
+    if (a.subpix) {
+        if (a.amode != A_CONV3 || a.upsample || a.stride != 1 || a.A2 || a.A3 || a.Cin % 64 || a.K != 4 * a.Cin ||
+            a.Ho != 2 * a.Hin || a.Wo != 2 * a.Win || a.M != a.Bn * a.Ho * a.Wo || a.res || a.row_part ||
+            a.ln_part || a.geglu || a.out_mode != OUT_F16 || (a.N & 7) || (a.M >> 2) % kCfgs[ci].mt ||
+            (splits > 1 && !fix) || (a.stats && a.stats_hw != a.Ho * a.Wo))
+            return hipErrorInvalidValue;
+        if (a.stats) a.stats_hw = a.Hin * a.Win;  // the kernel counts rows within a phase
+    }
     if (a.amode == A_CONV3 && a.A2 &&
         (a.K1 != 9 * a.Cin || a.K1 % 64 || a.K2 % 64 || a.K % 64 || a.K2 <= a.K1 || a.K <= a.K1 ||
          (a.A3 && a.K2 >= a.K) || a.stride != 1 || a.upsample || a.Ho != a.Hin || a.Wo != a.Win ||
@@ -1237,7 +1277,7 @@ hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s) {
     if (splits > 1 && ws == nullptr) return hipErrorInvalidValue;
     // operands are addressed with 32-bit byte offsets (buffer resources)
     const int64_t lim = 0x7fffffff;
-    if (2 * (int64_t)a.N * a.K > lim) return hipErrorInvalidValue;
+    if ((a.subpix ? 8 : 2) * (int64_t)a.N * a.K > lim) return hipErrorInvalidValue;
     if (a.amode == A_DENSE && (2 * (int64_t)a.M * a.lda > lim || (a.A2 && 2 * (int64_t)a.M * a.lda2 > lim)))
         return hipErrorInvalidValue;
     if (a.amode == A_CONV3 && (2 * (int64_t)a.Bn * a.Hin * a.Win * a.Cin > lim ||
@@ -1256,8 +1296,11 @@ hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s) {
                                               : 2.0 * a.M * a.K;
     const double out_bytes = (double)a.M * nout * (a.out_mode == OUT_F16 ? 2.0 : 4.0) +
                              (a.res ? 2.0 * a.M * nout : 0.0);
-    const double flops = 2.0 * a.M * a.N * a.K;
-    const double k_bytes = a_bytes + 2.0 * a.N * a.K + out_bytes;
+    // (the sub-pixel conv is counted as the 3x3 conv it computes: 9 taps of Cin, the 3x3
+    // weights; it issues 4 / 9 of those FLOPs)
+    const double kop = a.subpix ? 9.0 * a.Cin : (double)a.K;
+    const double flops = 2.0 * a.M * a.N * kop;
+    const double k_bytes = a_bytes + 2.0 * a.N * kop + out_bytes;
     launch_timed(kNames[ci][a.amode == A_CONV3], flops, k_bytes, [&] {
         if (a.amode == A_DENSE) launch_cfg<A_DENSE>(ci, grid, a, s);
         else launch_cfg<A_CONV3>(ci, grid, a, s);

@@ -544,6 +544,31 @@ hipError_t fold_shortcut_launch(const f16* w2, const f16* b2, const f16* ws, con
     return hipGetLastError();
 }
 
+// Sub-pixel weights (GemmArgs::subpix): block (o, phase), thread c over the input
+// channels; each of the 4 taps (ty, tx) sums the 1, 2 or 4 source taps (ky, kx) with
+// ty = (py + ky + 1) / 2 - py, tx = (px + kx + 1) / 2 - px in fp32.
+__global__ void fold_subpix_kernel(const f16* w3, f16* w4, int Co, int Ci) {
+    const int o = blockIdx.x, ph = blockIdx.y, py = ph >> 1, px = ph & 1;
+    for (int c = threadIdx.x; c < Ci; c += blockDim.x) {
+        float t[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ky = 0; ky < 3; ++ky)
+#pragma unroll
+            for (int kx = 0; kx < 3; ++kx) {
+                const int ty = (py + ky + 1) / 2 - py, tx = (px + kx + 1) / 2 - px;
+                t[ty * 2 + tx] += (float)w3[((int64_t)o * 9 + ky * 3 + kx) * Ci + c];
+            }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) w4[(((int64_t)ph * Co + o) * 4 + q) * Ci + c] = (f16)t[q];
+    }
+}
+
+hipError_t fold_subpix_launch(const f16* w3, f16* w4, int Co, int Ci, hipStream_t s) {
+    if (Co <= 0 || Ci <= 0) return hipErrorInvalidValue;
+    SDU_LAUNCH(fold_subpix_kernel, dim3(Co, 4), dim3(256), 0, s, w3, w4, Co, Ci);
+    return hipGetLastError();
+}
+
 // LayerNorm affine folded into the Linear after it, one block per output row n:
 // Wf[n, k] = fp16(gamma[k] W[n, k]), sf[n] = sum_k Wf[n, k] (of the rounded values the
 // GEMM multiplies), bf[n] = b[n] + sum_k beta[k] W[n, k].

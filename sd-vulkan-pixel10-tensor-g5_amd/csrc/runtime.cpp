@@ -123,6 +123,7 @@ int build_inventory(Ctx& c) {
     c.widx.clear();
     c.resnets.clear();
     c.xfs.clear();
+    c.ups.clear();
     c.tproj_total = c.kv_total = 0;
 
     bd.add("time_embedding.linear_1.weight", {kTembDim, kTembIn}, WK_LINEAR);
@@ -171,6 +172,7 @@ int build_inventory(Ctx& c) {
         if (i < 3) {
             snprintf(pf, sizeof pf, "up_blocks.%d.upsamplers.0.conv", i);
             bd.conv3(pf, cout, cout);
+            c.ups.push_back({pf, cout});
         }
     }
     bd.norm("conv_norm_out", 320);
@@ -224,6 +226,11 @@ int build_inventory(Ctx& c) {
         off_rfold[i] = top;
         top += align((int64_t)rd.cout * (9 * rd.cout + rd.cin)) + align(rd.cout);
     }
+    std::vector<int64_t> off_up(c.ups.size());
+    for (size_t i = 0; i < c.ups.size(); ++i) {
+        off_up[i] = top;
+        top += align(16 * (int64_t)c.ups[i].c * c.ups[i].c);
+    }
     c.wpool_bytes = (size_t)top * sizeof(f16);
     hipError_t e = hipMalloc(&c.wpool, c.wpool_bytes);
     if (e != hipSuccess) return set_err(&c, SDU_ERR_OOM, "weight pool allocation failed");
@@ -253,6 +260,7 @@ int build_inventory(Ctx& c) {
         c.weights[c.widx[b + ".attn2.to_v.weight"]].dev = c.w_kv + (int64_t)(xd.kv_off + xd.c) * kCtxDim;
         xf_fold(xd.c, &xd, P + off_fold[i]);
     }
+    for (size_t i = 0; i < c.ups.size(); ++i) c.ups[i].w4 = P + off_up[i];
     return SDU_OK;
 }
 
@@ -263,6 +271,11 @@ int fold_weights(Ctx& c, const std::string& name) {
         hipError_t e = fold_shortcut_launch(c.wd(rd.pf + ".conv2.weight"), c.wd(rd.pf + ".conv2.bias"),
                                             c.wd(rd.pf + ".conv_shortcut.weight"), c.wd(rd.pf + ".conv_shortcut.bias"),
                                             rd.w2sc, rd.b2sc, rd.cout, rd.cout, rd.cin, c.stream);
+        if (e != hipSuccess) return set_err(&c, SDU_ERR_HIP, std::string("weight fold: ") + hipGetErrorString(e));
+    }
+    for (const UpDesc& u : c.ups) {
+        if (!name.empty() && name.compare(0, u.pf.size() + 1, u.pf + ".") != 0) continue;
+        hipError_t e = fold_subpix_launch(c.wd(u.pf + ".weight"), u.w4, u.c, u.c, c.stream);
         if (e != hipSuccess) return set_err(&c, SDU_ERR_HIP, std::string("weight fold: ") + hipGetErrorString(e));
     }
     for (const XfDesc& xd : c.xfs) {

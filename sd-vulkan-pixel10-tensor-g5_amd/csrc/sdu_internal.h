@@ -89,6 +89,15 @@ struct GemmArgs {
     int lda3;
     int K2;           // (K when A3 == nullptr)
     int Bn, Hin, Win, Cin, Ho, Wo, stride, upsample;  // conv geometry
+    // Sub-pixel form of a 3x3 conv (pad 1) over the 2x nearest upsampling of A
+    // (subpix = 1; upsample = 0, stride 1, A the [Bn, Hin, Win, Cin] input, Ho = 2 Hin,
+    // Wo = 2 Win, Cin % 64 == 0): output pixel (2y + py, 2x + px) only sees input rows
+    // y + py - 1 + {0, 1} and columns x + px - 1 + {0, 1}, so each of the four phases
+    // (py, px) is a 2x2 conv of the input with summed taps (fold_subpix_launch): Wt is
+    // [4 phases][N][4 taps * Cin], K = 4 Cin, and GEMM row m = phase * (M / 4) + input
+    // pixel, stored at its output pixel.  M / 4 must be a multiple of the tile rows
+    // (the planner's choice); no residual, fp16 output, no split-K reduce launch.
+    int subpix;
     // B operand: W [N, K] row-major
     const f16* Wt;
     // epilogue
@@ -152,6 +161,12 @@ const char* gemm_kernel_name(const GemmArgs& a);  // tile variant the launch wil
 hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s);
 // Sum a.splits fp32 partials [splits][M][N] at a.partial and run the epilogue.
 hipError_t splitk_reduce_launch(const GemmArgs& a, double bytes, hipStream_t s);
+// Sub-pixel weights of a 3x3 conv that follows a 2x nearest upsampling (GemmArgs::subpix):
+// w3 [Cout][3][3][Cin] -> w4 [4 phases][Cout][2][2][Cin], phase = 2 py + px.  Tap (ty, tx)
+// of phase (py, px) is the fp32 sum of the 3x3 taps (ky, kx) with ty = (py + ky + 1) / 2 - py
+// and tx = (px + kx + 1) / 2 - px (upsampled row 2y + py - 1 + ky is input row
+// y + py - 1 + ty), rounded to fp16 once.
+hipError_t fold_subpix_launch(const f16* w3, f16* w4, int Cout, int Cin, hipStream_t s);
 
 // y[n] = act_out( sum_k act_in(x[k]) * W[n,k] + bias[n] ), fp32 in/out, W fp16 [N,K].
 // act: 0 none, 1 SiLU.  nvec vectors: x [nvec][K] -> y [nvec][N], up to 4 per launch

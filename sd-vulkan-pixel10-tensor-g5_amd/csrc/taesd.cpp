@@ -80,6 +80,10 @@ static int fold_out(Ctx& c, AuxNet& n) {
     if ((e = hipMemcpy(n.w_out2, hw.data(), hw.size() * 2, hipMemcpyHostToDevice)) ||
         (e = hipMemcpy(n.b_out2, bf, sizeof bf, hipMemcpyHostToDevice)))
         return hip_fail(c, e, "taesd fold");
+    for (int s = 0; s < 3; ++s)
+        if ((e = fold_subpix_launch(n.wd(L(p.up_conv[s]) + ".weight"), n.w4[s], kCh, kCh, c.stream)))
+            return hip_fail(c, e, "taesd fold");
+    if ((e = hipStreamSynchronize(c.stream))) return hip_fail(c, e, "taesd fold");
     return SDU_OK;
 }
 
@@ -87,12 +91,16 @@ int taesd_create(Ctx& c, const char* weights_dir, uint64_t seed, int flags) {
     AuxNet* n = new AuxNet();
     n->kind = AUX_TAESD;
     taesd_register(*n);
-    const size_t wout_n = 3 * 9 * kCh;
-    int st = aux_alloc(c, *n, (wout_n * 2 + 255) / 256 * 256 + 256);
+    // extra pool space: conv_out with the output affine, its fp32 bias, and the upsampling
+    // convs' sub-pixel weights [4][64][2][2][64]
+    const size_t wout_n = 3 * 9 * kCh, wout_b = (wout_n * 2 + 255) / 256 * 256, w4_b = 16 * kCh * kCh * 2;
+    const size_t extra_b = wout_b + 256 + 3 * w4_b;
+    int st = aux_alloc(c, *n, extra_b);
     if (st) { aux_free(n); return st; }
-    char* extra = (char*)n->pool + (n->pool_bytes - ((wout_n * 2 + 255) / 256 * 256 + 256));
+    char* extra = (char*)n->pool + (n->pool_bytes - extra_b);
     n->w_out2 = (f16*)extra;
-    n->b_out2 = (float*)(extra + (wout_n * 2 + 255) / 256 * 256);
+    n->b_out2 = (float*)(extra + wout_b);
+    for (int s = 0; s < 3; ++s) n->w4[s] = (f16*)(extra + wout_b + 256 + s * w4_b);
     const bool affine = (flags & SDU_INIT_RANDOM_AFFINE) != 0;
     for (const WeightRec& r : n->weights) {
         st = weights_dir ? load_weight_file(c, r, weights_dir) : gen_weight(c, r, seed, affine, kConvStd);
@@ -105,8 +113,15 @@ int taesd_create(Ctx& c, const char* weights_dir, uint64_t seed, int flags) {
 }
 
 static void conv(Exec& E, const f16* x, int B, int h, int w, int cin, int ups, const f16* W, const f16* bias,
-                 const f16* res, f16* y) {
+                 const f16* res, f16* y, const f16* w4 = nullptr) {
     GemmArgs a = conv3_args(x, B, h, w, cin, kCh, 1, ups, W, y);
+    // after the 2x upsampling: the sub-pixel form where each phase's pixels fill whole tiles
+    if (ups && w4 && (B * h * w) % 64 == 0) {
+        a.upsample = 0;
+        a.subpix = 1;
+        a.K = 4 * cin;
+        a.Wt = w4;
+    }
     a.bias = bias;
     a.res = res;
     a.ldr = kCh;
@@ -134,7 +149,7 @@ static void taesd_body(Exec& E, AuxNet& n, AuxState& S) {
         }
         if (s < 3) {
             f16* up = act(2 * h, 2 * w);
-            conv(E, cur, B, h, w, kCh, 1, n.wd(L(p.up_conv[s]) + ".weight"), nullptr, nullptr, up);
+            conv(E, cur, B, h, w, kCh, 1, n.wd(L(p.up_conv[s]) + ".weight"), nullptr, nullptr, up, n.w4[s]);
             h *= 2;
             w *= 2;
             cur = up;

@@ -180,6 +180,16 @@ static Act transformer(Exec& E, const XfDesc& t, Act xa, int H, int Wd, const f1
 static Act conv3_block(Exec& E, const std::string& pf, const f16* x, int H, int Wd, int Cin, int Cout,
                        int stride, int ups) {
     GemmArgs a = conv3_args(x, E.B, H, Wd, Cin, Cout, stride, ups, W(E, pf + ".weight"), nullptr);
+    // after a 2x nearest upsampling: the sub-pixel form (4 taps per output pixel instead of 9)
+    // where each phase's input pixels fill whole tiles
+    if (ups && Cin % 64 == 0 && (E.B * H * Wd) % 64 == 0)
+        for (const UpDesc& u : E.c.ups)
+            if (u.pf == pf && u.c == Cin && Cout == Cin) {
+                a.upsample = 0;
+                a.subpix = 1;
+                a.K = 4 * Cin;
+                a.Wt = u.w4;
+            }
     f16* y = E.alloc<f16>((size_t)a.M * Cout);
     a.C = y;
     a.bias = W(E, pf + ".bias");

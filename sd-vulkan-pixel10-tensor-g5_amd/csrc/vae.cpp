@@ -98,7 +98,7 @@ static void vae_register(AuxNet& n) {
 // [conv2 | shortcut] weights and summed biases, and the fp32 to_out bias with to_v's bias
 // folded in (bo + Wo bv: the rows of the softmax sum to 1, so P (V + bv) = P V + bv).
 struct VaeExtra {
-    size_t w2sc_off[2], b2sc_off[2], bout_off, bytes;
+    size_t w2sc_off[2], b2sc_off[2], bout_off, w4_off[3], bytes;
 };
 static VaeExtra extra_layout() {
     VaeExtra x{};
@@ -110,6 +110,9 @@ static VaeExtra extra_layout() {
         x.b2sc_off[k] = take((size_t)co[k] * 2);
     }
     x.bout_off = take((size_t)kTop * 4);
+    // the upsampling convs' sub-pixel weights [4][C][2][2][C]
+    const std::vector<UpStage> plan = up_plan();
+    for (int i = 0; i < 3; ++i) x.w4_off[i] = take((size_t)16 * plan[i].cout * plan[i].cout * 2);
     x.bytes = top;
     return x;
 }
@@ -145,6 +148,14 @@ static int vae_fold(Ctx& c, AuxNet& n) {
     n.b_attn_out = (float*)(base + x.bout_off);
     if ((e = hipMemcpy(n.b_attn_out, bout.data(), kTop * 4, hipMemcpyHostToDevice)))
         return hip_fail(c, e, "vae fold");
+    const std::vector<UpStage> plan = up_plan();
+    for (int i = 0; i < 3; ++i) {
+        n.w4[i] = (f16*)(base + x.w4_off[i]);
+        const std::string u = "decoder.up_blocks." + std::to_string(i) + ".upsamplers.0.conv.weight";
+        if ((e = fold_subpix_launch(n.wd(u), n.w4[i], plan[i].cout, plan[i].cout, c.stream)))
+            return hip_fail(c, e, "vae fold");
+    }
+    if ((e = hipStreamSynchronize(c.stream))) return hip_fail(c, e, "vae fold");
     return SDU_OK;
 }
 
@@ -168,10 +179,17 @@ int vae_create(Ctx& c, const char* weights_dir, uint64_t seed, int flags) {
 }
 
 static f16* conv(Exec& E, AuxNet& n, const std::string& pf, Act x, int H, int W, int cin, int cout, int ups,
-                 Act* out_act) {
+                 Act* out_act, const f16* w4 = nullptr) {
     const int Ho = ups ? 2 * H : H, Wo = ups ? 2 * W : W;
     f16* y = E.alloc<f16>((size_t)E.B * Ho * Wo * cout);
     GemmArgs a = conv3_args(x.p, E.B, H, W, cin, cout, 1, ups, n.wd(pf + ".weight"), y);
+    // after the 2x upsampling: the sub-pixel form where each phase's pixels fill whole tiles
+    if (ups && w4 && cin % 64 == 0 && (E.B * H * W) % 64 == 0) {
+        a.upsample = 0;
+        a.subpix = 1;
+        a.K = 4 * cin;
+        a.Wt = w4;
+    }
     a.bias = n.wd(pf + ".bias");
     want_stats(E, a, Ho * Wo);
     gemm(E, "vae_conv3x3", a);
@@ -283,7 +301,7 @@ static void vae_body(Exec& E, AuxNet& n, AuxState& S) {
         }
         if (plan[i].up) {
             conv(E, n, "decoder.up_blocks." + std::to_string(i) + ".upsamplers.0.conv", x, h, w, plan[i].cout,
-                 plan[i].cout, 1, &x);
+                 plan[i].cout, 1, &x, n.w4[i]);
             h *= 2;
             w *= 2;
         }
