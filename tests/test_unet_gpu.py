@@ -159,14 +159,17 @@ def test_forward_b2_96(unet_engine, oracle_weights):
 
 def test_set_weight_refolds(unet_engine, oracle_weights):
     """Folded weights: a transformer's feed-forward output and proj_out run as one
-    GEMM, and so do a resnet's conv2 and 1x1 shortcut.  Setting any of their source
-    tensors through sdu_set_weight refolds them: the forward matches the oracle run
-    with the same new weights."""
+    GEMM, and so do a resnet's conv2 and 1x1 shortcut; the convs after the 2x
+    upsamplings run on sub-pixel weights folded from theirs (at a 32x32 latent the 8->16
+    and 16->32 upsamplings take that form).  Setting any of their source tensors through
+    sdu_set_weight refolds them: the forward matches the oracle run with the same new
+    weights."""
     pf = "up_blocks.3.attentions.1"
     rpf = "up_blocks.3.resnets.1"
     names = [pf + ".transformer_blocks.0.ff.net.2.weight", pf + ".transformer_blocks.0.ff.net.2.bias",
              pf + ".proj_out.weight", pf + ".proj_out.bias",
-             rpf + ".conv2.weight", rpf + ".conv2.bias", rpf + ".conv_shortcut.weight", rpf + ".conv_shortcut.bias"]
+             rpf + ".conv2.weight", rpf + ".conv2.bias", rpf + ".conv_shortcut.weight", rpf + ".conv_shortcut.bias",
+             "up_blocks.1.upsamplers.0.conv.weight", "up_blocks.2.upsamplers.0.conv.weight"]
     specs = {p.name: p for p in Wt.param_specs()}
     rng = np.random.default_rng(5)
     p2 = dict(oracle_weights)
