@@ -1001,8 +1001,10 @@ void gemm_kernel(GemmArgs a) {
 // (tap-major, as W's K index) with fp16 dot products into fp32, the weights staged
 // in LDS (dynamic, CO * 9 * Cin * 2 bytes); the 16 slices of a pixel are consecutive
 // lanes, added by shuffles, and the first runs the common epilogue.  Loads go in
-// batches of 12 chunks (two batches at Cin = 320), all issued before any is used.
-constexpr int kNarrowPix = 16, kNarrowSlices = 16, kNarrowBatch = 12;
+// batches of 12 chunks (two batches at Cin = 320), all issued before any is used.  A
+// block takes 16-pixel groups g, g + gridDim.x, ... (at most kNarrowBlocks blocks), so on
+// large images (the VAE's 512x512 conv_out) the staged weights serve many groups.
+constexpr int kNarrowPix = 16, kNarrowSlices = 16, kNarrowBatch = 12, kNarrowBlocks = 2048;
 template <int CO>
 __global__ __launch_bounds__(256) void conv3_narrow_kernel(GemmArgs a) {
     if (a.c_ind) a.C = *a.c_ind;
@@ -1027,46 +1029,50 @@ __global__ __launch_bounds__(256) void conv3_narrow_kernel(GemmArgs a) {
     }
     __syncthreads();
     const int tid = threadIdx.x, sl = tid % kNarrowSlices;
-    const int p = blockIdx.x * kNarrowPix + tid / kNarrowSlices;
-    const int m = min(p, a.M - 1);
-    const int hw = a.Ho * a.Wo, bb = m / hw, r = m - bb * hw, oy = r / a.Wo, ox = r - oy * a.Wo;
-    float acc[CO];
+    const int ngroups = (a.M + kNarrowPix - 1) / kNarrowPix;
+    for (int grp = blockIdx.x; grp < ngroups; grp += gridDim.x) {
+        const int p = grp * kNarrowPix + tid / kNarrowSlices;
+        const int m = min(p, a.M - 1);
+        const int hw = a.Ho * a.Wo, bb = m / hw, r = m - bb * hw, oy = r / a.Wo, ox = r - oy * a.Wo;
+        float acc[CO];
 #pragma unroll
-    for (int co = 0; co < CO; ++co) acc[co] = 0.f;
-    // chunks in batches: every load of a batch issued before any is used
-    for (int j0 = sl; j0 < nchunk; j0 += kNarrowSlices * kNarrowBatch) {
-        uint4 x[kNarrowBatch];
+        for (int co = 0; co < CO; ++co) acc[co] = 0.f;
+        // chunks in batches: every load of a batch issued before any is used
+        for (int j0 = sl; j0 < nchunk; j0 += kNarrowSlices * kNarrowBatch) {
+            uint4 x[kNarrowBatch];
 #pragma unroll
-        for (int u = 0; u < kNarrowBatch; ++u) {
-            const int j = j0 + u * kNarrowSlices;
-            const int tap = j / cpt, c8 = j - tap * cpt;
-            const int iy = oy + tap / 3 - 1, ix = ox + tap % 3 - 1;
-            x[u] = make_uint4(0, 0, 0, 0);
-            if (j < nchunk && iy >= 0 && iy < a.Hin && ix >= 0 && ix < a.Win)
-                x[u] = *(const uint4*)(a.A + (((int64_t)bb * a.Hin + iy) * a.Win + ix) * a.Cin + c8 * 8);
-        }
+            for (int u = 0; u < kNarrowBatch; ++u) {
+                const int j = j0 + u * kNarrowSlices;
+                const int tap = j / cpt, c8 = j - tap * cpt;
+                const int iy = oy + tap / 3 - 1, ix = ox + tap % 3 - 1;
+                x[u] = make_uint4(0, 0, 0, 0);
+                if (j < nchunk && iy >= 0 && iy < a.Hin && ix >= 0 && ix < a.Win)
+                    x[u] = *(const uint4*)(a.A + (((int64_t)bb * a.Hin + iy) * a.Win + ix) * a.Cin + c8 * 8);
+            }
 #pragma unroll
-        for (int u = 0; u < kNarrowBatch; ++u) {
-            const int j = j0 + u * kNarrowSlices;
-            if (j >= nchunk) break;
-            const half2v* xh = (const half2v*)&x[u];
+            for (int u = 0; u < kNarrowBatch; ++u) {
+                const int j = j0 + u * kNarrowSlices;
+                if (j >= nchunk) break;
+                const half2v* xh = (const half2v*)&x[u];
 #pragma unroll
-            for (int co = 0; co < CO; ++co) {
-                const uint4 w = wsm[co * nchunk + j];
-                const half2v* wh = (const half2v*)&w;
+                for (int co = 0; co < CO; ++co) {
+                    const uint4 w = wsm[co * nchunk + j];
+                    const half2v* wh = (const half2v*)&w;
 #pragma unroll
-                for (int q = 0; q < 4; ++q) acc[co] = __builtin_amdgcn_fdot2(xh[q], wh[q], acc[co], false);
+                    for (int q = 0; q < 4; ++q) acc[co] = __builtin_amdgcn_fdot2(xh[q], wh[q], acc[co], false);
+                }
             }
         }
+#pragma unroll
+        for (int co = 0; co < CO; ++co)
+#pragma unroll
+            for (int off = 1; off < kNarrowSlices; off <<= 1) acc[co] += __shfl_xor(acc[co], off);
+        if (sl == 0 && p < a.M) {
+#pragma unroll
+            for (int co = 0; co < CO; ++co)
+                if (co < a.N) epi_store(a, p, co, acc[co], 0.f, co);
+        }
     }
-#pragma unroll
-    for (int co = 0; co < CO; ++co)
-#pragma unroll
-        for (int off = 1; off < kNarrowSlices; off <<= 1) acc[co] += __shfl_xor(acc[co], off);
-    if (sl != 0 || p >= a.M) return;
-#pragma unroll
-    for (int co = 0; co < CO; ++co)
-        if (co < a.N) epi_store(a, p, co, acc[co], 0.f, co);
 }
 
 // The narrow conv takes a 3x3 conv when its weights (up to 8 outputs) fit 64 KB of LDS.
@@ -1225,7 +1231,7 @@ hipError_t gemm_launch(GemmArgs a, float* ws, hipStream_t s) {
         a.partial = nullptr;
         const int co = a.N <= 4 ? 4 : 8;
         const size_t lds = (size_t)co * 9 * a.Cin * 2;
-        const dim3 grid((a.M + kNarrowPix - 1) / kNarrowPix);
+        const dim3 grid(std::min((a.M + kNarrowPix - 1) / kNarrowPix, kNarrowBlocks));
         const double flops = 2.0 * a.M * a.N * a.K;
         const double bytes = 2.0 * a.Bn * a.Hin * a.Win * a.Cin + 2.0 * a.N * a.K +
                              (double)a.M * a.N * (a.out_mode == OUT_F16 ? 2.0 : 4.0) + (a.res ? 2.0 * a.M * a.N : 0.0);
