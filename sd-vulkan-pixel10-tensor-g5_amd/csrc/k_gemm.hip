@@ -69,15 +69,28 @@ __device__ __forceinline__ void wait_vmcnt_lgkm0() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0x0 << 8) | ((N >> 4) << 14));
 }
 
+// The same with the tiles issued after the one about to be read still in flight: at
+// most `ahead` (<= A) tiles of LPT DMA instructions each.
+template <int LPT, int A>
+__device__ __forceinline__ void wait_tiles(int ahead) {
+    if constexpr (A == 0) wait_vmcnt_lgkm0<0>();
+    else if (ahead >= A) wait_vmcnt_lgkm0<A * LPT>();
+    else wait_tiles<LPT, A - 1>(ahead);
+}
+
 // Sum the per-thread column statistics of a block over the threads that own the same
 // 8 columns (thread t owns chunk t % CPR; chunk c covers columns col0 + 8c ..) through
 // LDS and add them to the per-(image, channel) fp64 statistics, one atomic per value,
 // the sums spread over all threads (each one's NTH / CPR LDS reads issued together).
 // red must hold NTH * 32 floats and be free (the caller's last LDS use is complete
-// after the first barrier here).
+// after the first barrier here).  Value v of thread t sits at v * NTH + (t ^ v): the
+// stores (one v, consecutive t) and the loads (consecutive v, one t) both fall on
+// distinct banks (a thread-major layout, 32 floats per thread, put every lane of a
+// store on one bank).
 template <int NTH, int CPR>
 __device__ __forceinline__ void stats_flush(const GemmArgs& a, const float (&st)[2][2][8], int b0,
                                             int m_last, int col0, float* red) {
+    static_assert(NTH % 32 == 0, "swizzle stays within a row");
     const int tid = threadIdx.x;
     __syncthreads();
 #pragma unroll
@@ -85,7 +98,10 @@ __device__ __forceinline__ void stats_flush(const GemmArgs& a, const float (&st)
 #pragma unroll
         for (int q = 0; q < 2; ++q)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) red[tid * 32 + sl * 16 + q * 8 + e] = st[sl][q][e];
+            for (int e = 0; e < 8; ++e) {
+                const int v = sl * 16 + q * 8 + e;
+                red[v * NTH + (tid ^ v)] = st[sl][q][e];
+            }
     __syncthreads();
     const int nslot = m_last / a.stats_hw != b0 ? 2 : 1;
     // value v of chunk c: slot v / 16, sum (0) or sum of squares (1) = (v / 8) % 2, column v % 8
@@ -97,7 +113,7 @@ __device__ __forceinline__ void stats_flush(const GemmArgs& a, const float (&st)
         if ((v >> 4) >= nslot || col >= a.N) continue;
         float t = 0.f;
 #pragma unroll
-        for (int j = 0; j < NTH / CPR; ++j) t += red[(c + j * CPR) * 32 + v];
+        for (int j = 0; j < NTH / CPR; ++j) t += red[v * NTH + ((c + j * CPR) ^ v)];
         atomicAdd(&a.stats[((int64_t)(b0 + (v >> 4)) * a.N + col) * 2 + ((v >> 3) & 1)], (double)t);
     }
 }
@@ -570,10 +586,7 @@ void gemm_kernel(GemmArgs a) {
     }
     for (int kt = 0; kt < nk; ++kt) {
         // tile kt must have landed; the tiles issued after it may still be in flight
-        const int ahead = min(NS - 2, nk - 1 - kt);
-        if (ahead >= 2) wait_vmcnt_lgkm0<(NS >= 4 ? 2 * LPT : 0)>();
-        else if (ahead == 1) wait_vmcnt_lgkm0<LPT>();
-        else wait_vmcnt_lgkm0<0>();
+        wait_tiles<LPT, NS - 2>(min(NS - 2, nk - 1 - kt));
         __builtin_amdgcn_s_barrier();
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         // wave priority: highest while issuing the next tile's DMA, raised through this
@@ -839,6 +852,7 @@ void gemm_kernel(GemmArgs a) {
     const bool do_st = a.stats != nullptr && !narrow;
     // (sub-pixel conv: statistics rows counted within the phase, stats_hw = Hin * Win)
     const int st_b0 = do_st ? (m0 - sp_base) / a.stats_hw : 0;
+    const int st_mb = sp_base + (st_b0 + 1) * a.stats_hw;  // first row of the next image
     float st[2][2][8];
 #pragma unroll
     for (int sl = 0; sl < 2; ++sl)
@@ -957,7 +971,7 @@ void gemm_kernel(GemmArgs a) {
                     }
                 }
                 if (do_st) {
-                    const bool s1 = (m - sp_base) / a.stats_hw != st_b0;
+                    const bool s1 = m >= st_mb;
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         const float f = (float)oh[e];
